@@ -1,0 +1,115 @@
+/*
+ * tileinfer_amd.h — C ABI of the MI355X (gfx950) paged KV-cache library.
+ *
+ * The library implements tileInfer's paged KV-cache hot path as hand-written HIP kernels:
+ *   - the slot-mapped K/V append           (replaces kernels/kvcache_store.py:43-71, store_kvcache)
+ *   - single-query paged GQA decode        (replaces kernels/gqa_decode_paged.py:392-437,
+ *     attention with a split-K merge         gqa_decode_paged_fn)
+ *
+ * Conventions shared by every entry point
+ *   - All tensor pointers are DEVICE pointers owned by the caller. The library never allocates,
+ *     frees or synchronises inside a call: every call only enqueues kernels on `stream`.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream). Calls on different streams
+ *     are independent; a workspace buffer must not be shared by calls that can overlap.
+ *   - Strides are in ELEMENTS, not bytes.
+ *   - dtype codes: TI_DTYPE_BF16 or TI_DTYPE_F16 (the cache, key/value, q and out share it).
+ *   - Return value: TI_OK (0) on success, otherwise one of the TI_E* codes below; the text of the
+ *     most recent error on the calling thread is returned by ti_last_error().
+ */
+#ifndef TILEINFER_AMD_H_
+#define TILEINFER_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TI_DTYPE_BF16 0
+#define TI_DTYPE_F16 1
+
+#define TI_OK 0
+#define TI_EINVAL 1       /* bad argument: shape, stride, alignment or size out of range */
+#define TI_ELAUNCH 2      /* the HIP runtime rejected a launch or a device query */
+#define TI_EUNSUPPORTED 3 /* valid arguments that this build has no kernel for */
+
+/* Decode kernel variants (argument `variant` of ti_gqa_decode_paged). */
+#define TI_DECODE_AUTO 0   /* the measured-fastest variant for the shape */
+#define TI_DECODE_MFMA 1   /* query group packed into a 16-row MFMA tile, K/V direct to registers */
+#define TI_DECODE_SCALAR 2 /* K/V pages staged in LDS, fp32 FMA, DPP/shuffle softmax reductions */
+
+/*
+ * Slot-mapped K/V append: for every i in [0, n_tokens) with 0 <= slot_mapping[i] < num_slots,
+ *   k_cache[slot_mapping[i], 0:row_elems] = key[i, 0:row_elems]
+ *   v_cache[slot_mapping[i], 0:row_elems] = value[i, 0:row_elems]
+ * Rows whose slot is negative are skipped (the reference's padding convention); slots at or beyond
+ * num_slots are skipped as well instead of writing out of bounds. A bit copy: no arithmetic.
+ * Duplicate non-negative slots within one call are unsupported (the surviving row is unspecified).
+ *
+ * Replaces: store_kvcache(key, value, k_cache, v_cache, slot_mapping)
+ *           kernels/kvcache_store.py:43-71 (kernel body 14-40, torch semantics 74-84).
+ *   key/value        [n_tokens, row_elems] rows at key_row_stride / value_row_stride (the
+ *                    reference's key.reshape(N, num_heads*head_dim))
+ *   k_cache/v_cache  [num_slots, row_elems] rows at cache_row_stride (kernels/kvcache_store.py:55-56)
+ *   slot_mapping     [n_tokens] int32, -1 = skip (kernels/kvcache_store.py:57)
+ */
+int ti_kv_append(const void* key, const void* value, int64_t key_row_stride,
+                 int64_t value_row_stride, void* k_cache, void* v_cache, int64_t cache_row_stride,
+                 const int32_t* slot_mapping, int64_t n_tokens, int64_t row_elems, int64_t num_slots,
+                 int32_t dtype, void* stream);
+
+/*
+ * Launch plan of a paged decode call: the split-K partition length actually used, the maximum
+ * number of partitions per sequence, and the fp32 workspace the call needs (0 when every sequence
+ * fits one partition). `split_tokens` <= 0 asks the library to choose; a positive value is used as
+ * given after validation (a multiple of 32 and of page_size). The plan depends only on host-known
+ * bounds, so it is valid for any seqlen values <= max_blocks_per_seq * page_size and it is safe to
+ * compute once and reuse under graph capture.
+ *
+ * No reference counterpart: the reference decode has no split-K (kernels/gqa_decode_paged.py:73,
+ * one CTA per (sequence, KV head)); this is the sizing half of the split-K design.
+ */
+int ti_gqa_decode_plan(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                       int32_t page_size, int32_t max_blocks_per_seq, int32_t split_tokens,
+                       int32_t* split_tokens_out, int32_t* max_splits_out,
+                       int64_t* workspace_bytes_out);
+
+/*
+ * Paged GQA decode attention for one query token per sequence:
+ *   out[b, h, :] = softmax_j( q[b,h,:] . K_b[j,:] * head_dim^-0.5 ) @ V_b[j,:],  j < seqlen[b]
+ * where K_b[j] = k_cache[block_table[b, j / page_size], j % page_size, h / (Hq/Hkv), :] and V_b
+ * likewise. fp32 accumulation and softmax; output rounded to the input dtype (RNE).
+ * seqlen[b] == 0 gives a zero row. Block ids outside [0, num_blocks) at positions < seqlen[b]
+ * are treated as absent (masked, never loaded); entries at or beyond ceil(seqlen[b]/page_size)
+ * are never read, so the -1 padding of the reference's tables is harmless.
+ *
+ * Replaces: gqa_decode_paged_fn(q, k_cache, v_cache, block_table, seqlen_kv, page_size=16)
+ *           kernels/gqa_decode_paged.py:392-437 (math: ref_gqa_decode_paged, 444-461).
+ *   q            [batch, num_q_heads, head_dim], last dim contiguous, strides q_stride_b/_h
+ *   k/v_cache    [num_blocks, page_size, num_kv_heads, head_dim] contiguous (one layer's slab)
+ *   block_table  [batch, >= ceil(max seqlen / page_size)] int32, row stride block_table_stride;
+ *                max_blocks_per_seq bounds every seqlen: seqlen[b] <= max_blocks_per_seq*page_size
+ *   seqlen       [batch] int32 (the reference's seqlen_kv / context_lens)
+ *   out          [batch, num_q_heads, head_dim] contiguous
+ *   workspace    >= workspace_bytes from ti_gqa_decode_plan with the same arguments (may be NULL
+ *                when that is 0); contents need no initialisation.
+ *   split_tokens as in ti_gqa_decode_plan; variant one of TI_DECODE_*.
+ */
+int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+                        const void* v_cache, const int32_t* block_table, int64_t block_table_stride,
+                        const int32_t* seqlen, void* out, void* workspace, int64_t workspace_bytes,
+                        int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                        int32_t page_size, int64_t num_blocks, int32_t max_blocks_per_seq,
+                        int32_t split_tokens, int32_t variant, int32_t dtype, void* stream);
+
+/* Text of the last error reported on the calling thread ("" when none). */
+const char* ti_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int32_t ti_abi_version(void);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* TILEINFER_AMD_H_ */

@@ -1,0 +1,234 @@
+"""Parity of the HIP paged decode (ti_gqa_decode_paged) with the CPU oracle, plus the bitwise
+invariants the layout promises (shared vs private prefix, block permutation, padding)."""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (assert_decode_close, bits, cpu_step, flat, fp64_decode, gpu_step, say)
+from oracle.ref_torch import ref_gqa_decode_paged
+from tileinfer_amd.kernels.gqa_decode_paged import decode_plan, gqa_decode_paged_fn
+from tileinfer_amd.kernels.kvcache_store import store_kvcache
+from tileinfer_amd.workloads import PagedStep, config1, config2, config5, make_step
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+VARIANTS = ["mfma", "scalar"]
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("ctx", [512, 513])
+def test_config1_vs_oracle_and_golden(ctx, variant, dev):
+    say(f"decode config1 ctx={ctx} variant={variant}")
+    step = config1(ctx=ctx)
+    out, kc, vc = gpu_step(step, dev, variant=variant)
+    ref, k_ref, _ = cpu_step(step)
+    assert torch.equal(bits(kc.cpu()), bits(k_ref))
+    assert_decode_close(out, ref)
+    # Tighter against the exact value: the kernel keeps scores in fp32.
+    assert_decode_close(out, fp64_decode(step, k_ref, vc.cpu()), atol=4e-3, rtol=1e-2)
+    meta = json.loads((GOLDEN / f"config1_ctx{ctx}.json").read_text())
+    gold = torch.from_numpy(np.load(GOLDEN / f"config1_ctx{ctx}_out.npy")).view(torch.bfloat16)
+    assert_decode_close(out, gold.view(1, 24, 256))
+    assert meta["ctx"] == ctx
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_config2_vs_oracle(variant, dev):
+    step = config2()
+    say(f"decode config2 ctx={step.meta['ctx']} variant={variant}")
+    out, _, _ = gpu_step(step, dev, variant=variant)
+    ref, _, _ = cpu_step(step)
+    assert_decode_close(out, ref)
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_reference_selftest_shape(variant, dev):
+    """kernels/gqa_decode_paged.py:481-512 at reduced batch: Hq 32, Hkv 8, D 128, seqlen 8192,
+    a fifth of the batch shortened to U[2048, 8192), every sequence on the same sequential table."""
+    say(f"decode reference selftest shape variant={variant}")
+    g = torch.Generator().manual_seed(0)
+    b, hq, hkv, d, seqlen, ps = 10, 32, 8, 128, 8192, 16
+    max_pages = int(seqlen * 1.1) // ps
+    seq = torch.full((b,), seqlen, dtype=torch.int32)
+    seq[: b // 5] = torch.randint(seqlen // 4, seqlen, (b // 5,), generator=g, dtype=torch.int32)
+    q = torch.randn(b, hq, d, generator=g).to(torch.bfloat16)
+    kc = torch.randn(max_pages, ps, hkv, d, generator=g).to(torch.bfloat16)
+    vc = torch.randn(max_pages, ps, hkv, d, generator=g).to(torch.bfloat16)
+    table = torch.arange(max_pages, dtype=torch.int32).unsqueeze(0).expand(b, -1).contiguous()
+    out = gqa_decode_paged_fn(q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), seq.to(dev), ps,
+                              variant=variant)
+    ref = ref_gqa_decode_paged(q, kc, vc, table, seq, ps)
+    assert_decode_close(out, ref)
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_edge_lengths_and_splits(variant, dev):
+    """Context lengths around tile, page and partition boundaries, with a small partition so the
+    merge runs; ctx 0 must give zeros."""
+    ctx = [0, 1, 2, 15, 16, 17, 31, 32, 33, 255, 256, 257, 511, 512, 513, 1000]
+    say(f"decode edge lengths variant={variant} ctx={ctx}")
+    step = make_step(ctx, pool=300, seed=21)
+    for split in (256, None):
+        out, kc, vc = gpu_step(step, dev, variant=variant, split_tokens=split, append=False)
+        ref, _, _ = cpu_step(step, append=False)
+        assert_decode_close(out, ref)
+        assert not bool(out[0].float().abs().sum() != 0), "ctx 0 must give a zero row"
+        assert_decode_close(out, fp64_decode(step, step.k_cache, step.v_cache), atol=1e-2)
+
+
+def test_ctx1_and_constant_v(dev):
+    """Closed forms: ctx 1 returns V[0] of the mapped KV head; constant V returns that constant."""
+    say("decode closed forms")
+    step = make_step([1, 40, 300], pool=40, seed=3)
+    out, _, _ = gpu_step(step, dev, append=False)
+    g = 6
+    blk = int(step.block_table[0, 0])
+    v0 = step.v_cache[blk, 0]  # [Hkv, D]
+    expect = v0.repeat_interleave(g, dim=0)
+    assert torch.equal(bits(out[0].cpu()), bits(expect))
+    vc = torch.full_like(step.v_cache, 0.375)
+    out2 = gqa_decode_paged_fn(step.q.to(dev), step.k_cache.to(dev), vc.to(dev),
+                               step.block_table.to(dev), step.seqlen.to(dev))
+    assert bool((out2.float() == 0.375).all())
+
+
+def test_shared_vs_private_prefix_bitwise(dev):
+    """Sequences whose tables alias one prefix give bitwise the same output as private copies."""
+    say("decode shared vs private (config5 at batch 8)")
+    shared = config5(batch=8, device=dev, shared=True)
+    private = config5(batch=8, device=dev, shared=False)
+    for variant in VARIANTS:
+        o1 = gqa_decode_paged_fn(shared.q, shared.k_cache, shared.v_cache, shared.block_table,
+                                 shared.seqlen, variant=variant)
+        o2 = gqa_decode_paged_fn(private.q, private.k_cache, private.v_cache, private.block_table,
+                                 private.seqlen, variant=variant)
+        assert torch.equal(bits(o1), bits(o2)), variant
+    # And against the oracle for two sampled sequences (CPU copies of their blocks only).
+    for i in (0, 5):
+        pages = shared.block_table[i].long()
+        sub = PagedStep(q=shared.q[i:i + 1].cpu(), k_new=shared.k_new[i:i + 1].cpu(),
+                        v_new=shared.v_new[i:i + 1].cpu(), slot_mapping=shared.slot_mapping[i:i + 1].cpu(),
+                        block_table=torch.arange(len(pages), dtype=torch.int32).view(1, -1),
+                        seqlen=shared.seqlen[i:i + 1].cpu(), k_cache=shared.k_cache[pages].cpu(),
+                        v_cache=shared.v_cache[pages].cpu())
+        ref, _, _ = cpu_step(sub, append=False)
+        assert_decode_close(o1[i:i + 1], ref)
+
+
+def test_block_permutation_and_padding_bitwise(dev):
+    """Renaming physical blocks, or widening the table with -1 columns, changes no output bit."""
+    say("decode block permutation / padding invariance")
+    step = make_step([700, 1234, 65, 2048], pool=400, seed=8)
+    base, _, _ = gpu_step(step, dev, append=False)
+    g = torch.Generator().manual_seed(9)
+    perm = torch.randperm(400, generator=g)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(400)
+    kc2 = step.k_cache[inv]  # block j moves to perm[j]
+    vc2 = step.v_cache[inv]
+    tbl = step.block_table.clone()
+    live = tbl >= 0
+    tbl[live] = perm[tbl[live].long()].to(torch.int32)
+    out2 = gqa_decode_paged_fn(step.q.to(dev), kc2.to(dev), vc2.to(dev), tbl.to(dev),
+                               step.seqlen.to(dev))
+    assert torch.equal(bits(base), bits(out2))
+    wide = torch.full((4, tbl.shape[1] + 37), -1, dtype=torch.int32)
+    wide[:, :tbl.shape[1]] = tbl
+    out3 = gqa_decode_paged_fn(step.q.to(dev), kc2.to(dev), vc2.to(dev), wide.to(dev),
+                               step.seqlen.to(dev), split_tokens=decode_plan(4, 24, 4, 256, 16, tbl.shape[1])[0])
+    assert torch.equal(bits(base), bits(out3))
+
+
+def test_invalid_block_ids_are_masked(dev):
+    """A block id outside the cache at a used position is treated as absent (never read)."""
+    say("decode invalid block ids")
+    step = make_step([100, 100], pool=20, seed=4)
+    tbl = step.block_table.clone()
+    tbl[0, 2] = 10**6      # page 2 (tokens 32..47) of sequence 0 -> absent
+    tbl[1, 0] = -5         # page 0 (tokens 0..15) of sequence 1 -> absent
+    out = gqa_decode_paged_fn(step.q.to(dev), step.k_cache.to(dev), step.v_cache.to(dev),
+                              tbl.to(dev), step.seqlen.to(dev))
+    # Expected: attention over the remaining positions only (fp64, built by hand).
+    kf = step.k_cache.float().reshape(-1, 4, 256)
+    vf = step.v_cache.float().reshape(-1, 4, 256)
+    for b, gone in ((0, range(32, 48)), (1, range(0, 16))):
+        pos = [p for p in range(100) if p not in gone]
+        rows = torch.tensor([int(step.block_table[b, p // 16]) * 16 + p % 16 for p in pos])
+        k, v = kf[rows].double(), vf[rows].double()
+        for h in range(24):
+            s = k[:, h // 6] @ step.q[b, h].double() / 16.0
+            w = torch.softmax(s, 0)
+            torch.testing.assert_close(out[b, h].double().cpu(), w @ v[:, h // 6],
+                                       atol=1e-2, rtol=1e-2)
+
+
+def test_determinism_and_split_invariance(dev):
+    say("decode determinism / split sizes")
+    step = make_step([3000, 5000, 1, 4097], pool=900, seed=12)
+    a, _, _ = gpu_step(step, dev, append=False)
+    b, _, _ = gpu_step(step, dev, append=False)
+    assert torch.equal(bits(a), bits(b))
+    ref, _, _ = cpu_step(step, append=False)
+    for split in (32, 64, 256, 1024, 2048, 8192):
+        o, _, _ = gpu_step(step, dev, append=False, split_tokens=split)
+        assert_decode_close(o, ref)
+
+
+def test_fp16(dev):
+    say("decode fp16")
+    step = make_step([333, 1500], pool=150, seed=14, dtype=torch.float16)
+    for variant in VARIANTS:
+        out, _, _ = gpu_step(step, dev, variant=variant)
+        ref, _, _ = cpu_step(step)
+        assert out.dtype == torch.float16
+        assert_decode_close(out, ref)
+
+
+def test_long_context_32k(dev):
+    """Two sequences of config 3's shape (32,768 tokens, randomly permuted blocks)."""
+    say("decode 2 x 32768")
+    step = make_step([32768, 32768], pool=4096, seed=1003)
+    out, _, _ = gpu_step(step, dev)
+    ref, _, _ = cpu_step(step)
+    assert_decode_close(out, ref)
+
+
+def test_graph_capture_replay(dev):
+    """Append + decode captured in a HIP graph; every replay matches the eager result."""
+    say("graph capture")
+    step = make_step([900, 77, 2500], pool=300, seed=31)
+    kc = step.k_cache.to(dev)
+    vc = step.v_cache.to(dev)
+    q = step.q.to(dev)
+    kn, vn = step.k_new.to(dev), step.v_new.to(dev)
+    slots = step.slot_mapping.to(dev)
+    tbl = step.block_table.to(dev)
+    seq = step.seqlen.to(dev)
+
+    def fn():
+        store_kvcache(kn, vn, flat(kc), flat(vc), slots)
+        return gqa_decode_paged_fn(q, kc, vc, tbl, seq)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = fn()
+    gen = torch.Generator(device=dev).manual_seed(2)
+    for r in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen, device=dev).to(q.dtype))
+        kn.copy_(torch.randn(kn.shape, generator=gen, device=dev).to(kn.dtype))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = fn()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(static_out), bits(eager)), f"replay {r}"

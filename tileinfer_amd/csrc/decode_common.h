@@ -1,0 +1,77 @@
+// Definitions shared by the paged decode kernels (MFMA and scalar variants).
+#pragma once
+
+#include <math.h>
+
+#include "ti_common.h"
+
+namespace ti {
+
+constexpr int kMaxSplitPages = 512;  // block ids of one partition staged in LDS
+constexpr int kMaxSplitTokens = 8192;
+
+struct Bf16 {};
+struct F16 {};
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c, Bf16) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c, F16) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// Two floats -> two 16-bit values (round to nearest even), x in the low half.
+__device__ __forceinline__ uint32_t pack2(float x, float y, Bf16) {
+  bf16x2_t v = {static_cast<__bf16>(x), static_cast<__bf16>(y)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ uint32_t pack2(float x, float y, F16) {
+  f16x2_t v = {static_cast<_Float16>(x), static_cast<_Float16>(y)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ u32x4 load16(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+struct DecodeArgs {
+  const uint16_t* q;
+  int64_t q_sb, q_sh;  // q strides (elements)
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  int64_t page_stride;  // elements per physical block: page_size * hkv * D
+  int64_t row_stride;   // elements per token row: hkv * D
+  const int32_t* block_table;
+  int64_t bt_stride;
+  const int32_t* seqlen;
+  uint16_t* out;   // [B, hq, D]
+  float* part_o;   // [B, hq, max_splits, D]
+  float* part_ml;  // [B, hq, max_splits, 2]  (running max in log2 units, sum of exp2)
+  int64_t num_blocks;
+  int32_t hq, hkv, group, page_size, max_blocks, max_splits, split_tokens;
+  float scale_log2;
+};
+
+// Clamped context length of sequence b and its number of partitions.
+__device__ __forceinline__ int seq_len(const DecodeArgs& a, int b) {
+  int ctx = a.seqlen[b];
+  const int cap = a.max_blocks * a.page_size;
+  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+  return ctx;
+}
+
+
+// Launches the LDS-staged scalar variant of the partial kernel (gqa_decode_scalar.hip).
+int launch_decode_scalar(const DecodeArgs& a, int batch, bool bf16, int head_dim,
+                         hipStream_t stream);
+
+}  // namespace ti

@@ -1,0 +1,476 @@
+// Paged GQA decode attention with split-K for gfx950 (MI355X).
+//
+// Replaces tileInfer's gqa_decode_paged_fn (kernels/gqa_decode_paged.py:392-437), whose TileLang
+// kernels run one CTA per (sequence, KV head) over the whole context (44-177, 191-367). Here the
+// context of every (sequence, KV head) is cut into split-K partitions; one wavefront owns one
+// (sequence, KV head, partition), and the waves of a workgroup are the KV heads of one
+// (sequence, partition), so a workgroup streams whole 2 KiB token rows (all KV heads) of each
+// page. Partitions write unnormalised (m, l, o) partials that a second kernel merges in a fixed
+// order; a sequence that fits one partition is normalised and written directly.
+//
+// Math (the reference's recipe, ref_gqa_decode_paged, kernels/gqa_decode_paged.py:444-461):
+//   s_j = q . k_j * D^-1/2 ;  p = softmax(s) ;  o = p @ V,
+// evaluated with an online softmax in base 2 (scores pre-scaled by D^-1/2 * log2 e, as the
+// reference kernel does at 50 and 138-142), fp32 accumulation, P rounded to the cache dtype before
+// the P.V product (as the reference kernel does at 148 and the torch recipe at 459-460).
+//
+// MFMA layout (v_mfma_f32_16x16x32_{bf16,f16}, lane l: row/col l%16, k-group l/16 of 8 values):
+//   S^T[16 tokens x 16 heads] = K[16 tokens x 32 d] . Q^T[32 d x 16 heads]   (D/32 steps)
+//     A = K rows straight from the page (lane (m,g): token m, d in [32kk+8g, +8)),
+//     B = the query group, rows >= group are zero; C leaves lane (n,g) holding tokens 4g..4g+3
+//     of head n.
+//   O^T[16 d x 16 heads] += V^T[16 d x 32 tokens] . P^T[32 tokens x 16 heads]  (D/16 tiles)
+//     B = P taken as-is from the S^T accumulators of two 16-token sub-tiles (no transpose),
+//     A = V rows gathered so that lane (m,g) owns d = 128c+8m+e (e < 8) of the same 8 tokens,
+//     assembled with v_perm_b32; C leaves lane (n,g) holding head n, d in [128c+32g, +32).
+// The head of every O^T accumulator is its lane's head, so the softmax rescale needs no
+// cross-lane traffic; only the running max crosses the 4 lanes that share a head.
+#include "decode_common.h"
+
+namespace ti {
+namespace {
+
+template <int D>
+struct Tile {
+  static constexpr int KK = D / 32;   // q.k MFMA steps
+  static constexpr int NC = D / 128;  // 16-byte d-chunks per lane per V row
+  u32x4 k[2][KK];                     // [sub-tile][k-step]
+  u32x4 v[2][4][NC];                  // [sub-tile][row 4g+r][chunk]
+};
+
+template <int D, typename Tag, int WPB>
+__global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
+  constexpr int KK = D / 32;
+  constexpr int NC = D / 128;
+  constexpr int NT = D / 16;
+  static_assert(D % 128 == 0, "head_dim must be a multiple of 128");
+
+  __shared__ int s_bids[kMaxSplitPages];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n = lane & 15;  // MFMA row/col index: token row of K, head of S^T/O^T, d-col of V^T
+  const int g = lane >> 4;  // MFMA k-group
+  const int kvh = blockIdx.x * WPB + wave;
+  const int split = blockIdx.y;
+  const int b = blockIdx.z;
+
+  const int ctx = seq_len(a, b);
+  const int nsplit = (ctx + a.split_tokens - 1) / a.split_tokens;
+  if (split >= (nsplit > 0 ? nsplit : 1)) return;  // uniform over the workgroup
+  const int tok0 = split * a.split_tokens;
+  const int tok1 = min(tok0 + a.split_tokens, ctx);
+  const int page0 = tok0 / a.page_size;
+  const int npages = tok1 > tok0 ? (tok1 - tok0 + a.page_size - 1) / a.page_size : 0;
+  for (int i = threadIdx.x; i < npages; i += 64 * WPB) {
+    s_bids[i] = a.block_table[b * a.bt_stride + page0 + i];
+  }
+  __syncthreads();
+
+  const int h = kvh * a.group + n;
+  const bool head_ok = n < a.group;
+
+  // Query group as the B operand of S^T = K . Q^T; rows beyond the group stay zero.
+  u32x4 qop[KK];
+  {
+    const uint16_t* qrow = a.q + b * a.q_sb + int64_t(h) * a.q_sh;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      qop[kk] = head_ok ? load16(qrow + 32 * kk + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  const int64_t lane_k = int64_t(n) * a.row_stride + kvh * D + 8 * g;
+  const int64_t lane_v = int64_t(4 * g) * a.row_stride + kvh * D + 8 * n;
+
+  f32x4 o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+
+  // Loads one 32-token tile (two 16-token sub-tiles) at position t0 into `T`; returns a bit mask
+  // of the sub-tiles that are present (in range and with a valid block id).
+  auto load_tile = [&](Tile<D>& T, int t0) -> int {
+    int present = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = t0 + 16 * i;
+      int bid = -1;
+      if (p < tok1) bid = __builtin_amdgcn_readfirstlane(s_bids[(p - tok0) / a.page_size]);
+      if (p < tok1 && bid >= 0 && bid < a.num_blocks) {
+        present |= 1 << i;
+        const int64_t base = int64_t(bid) * a.page_stride + int64_t(p % a.page_size) * a.row_stride;
+        const uint16_t* kb = a.k_cache + base + lane_k;
+        const uint16_t* vb = a.v_cache + base + lane_v;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) T.k[i][kk] = load16(kb + 32 * kk);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) T.v[i][r][c] = load16(vb + r * a.row_stride + 128 * c);
+        }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) T.k[i][kk] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) T.v[i][r][c] = u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+    }
+    return present;
+  };
+
+  auto compute_tile = [&](Tile<D>& T, int t0, int present) {
+    // Rows past the partition end belong to the same page but carry no (or another
+    // partition's) token: zero their V so that 0 * garbage cannot reach the accumulators.
+    if (t0 + 32 > tok1) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (t0 + 16 * i + 4 * g + r >= tok1) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) T.v[i][r][c] = u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+      }
+    }
+    f32x4 s[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      s[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) s[i] = mfma16x16x32(T.k[i][kk], qop[kk], s[i], Tag{});
+    }
+    float sv[8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = t0 + 16 * i + 4 * g + r;
+        const bool ok = ((present >> i) & 1) && tok < tok1;
+        sv[4 * i + r] = ok ? s[i][r] * a.scale_log2 : -INFINITY;
+      }
+    }
+    float mx = sv[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - m_use);
+    float p[8];
+    float psum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[j] = fast_exp2(sv[j] - m_use);
+      psum += p[j];
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) o[t] *= alpha;
+    }
+    // P^T operand: element j <-> token (sub-tile j/4, row 4g + j%4).
+    u32x4 pop;
+    pop[0] = pack2(p[0], p[1], Tag{});
+    pop[1] = pack2(p[2], p[3], Tag{});
+    pop[2] = pack2(p[4], p[5], Tag{});
+    pop[3] = pack2(p[6], p[7], Tag{});
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        u32x4 vop;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int i = k >> 1;
+          const int r = 2 * (k & 1);
+          vop[k] = __builtin_amdgcn_perm(T.v[i][r + 1][c][e >> 1], T.v[i][r][c][e >> 1], sel);
+        }
+        o[8 * c + e] = mfma16x16x32(vop, pop, o[8 * c + e], Tag{});
+      }
+    }
+  };
+
+  const int ntiles = (tok1 - tok0 + 31) / 32;
+  if (ntiles > 0) {
+    Tile<D> ta, tb;
+    int pa = load_tile(ta, tok0);
+    int it = 0;
+    for (; it + 2 <= ntiles; it += 2) {
+      const int t0 = tok0 + 32 * it;
+      int pb = load_tile(tb, t0 + 32);
+      compute_tile(ta, t0, pa);
+      if (it + 2 < ntiles) pa = load_tile(ta, t0 + 64);
+      compute_tile(tb, t0 + 32, pb);
+    }
+    if (it < ntiles) compute_tile(ta, tok0 + 32 * it, pa);
+  }
+
+  // Sum the per-lane partial denominators of each head (lanes n, n+16, n+32, n+48).
+  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  if (!head_ok) return;
+
+  if (nsplit <= 1) {
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    uint16_t* orow = a.out + (int64_t(b) * a.hq + h) * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        u32x4 w;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          w[k] = pack2(o[8 * c + 2 * k][r] * inv, o[8 * c + 2 * k + 1][r] * inv, Tag{});
+        }
+        *reinterpret_cast<u32x4*>(orow + 128 * c + 32 * g + 8 * r) = w;
+      }
+    }
+  } else {
+    const int64_t slot = (int64_t(b) * a.hq + h) * a.max_splits + split;
+    float* prow = a.part_o + slot * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        f32x4 w0 = {o[8 * c + 0][r], o[8 * c + 1][r], o[8 * c + 2][r], o[8 * c + 3][r]};
+        f32x4 w1 = {o[8 * c + 4][r], o[8 * c + 5][r], o[8 * c + 6][r], o[8 * c + 7][r]};
+        f32x4* dst = reinterpret_cast<f32x4*>(prow + 128 * c + 32 * g + 8 * r);
+        dst[0] = w0;
+        dst[1] = w1;
+      }
+    }
+    if (g == 0) {
+      a.part_ml[2 * slot] = m_run;
+      a.part_ml[2 * slot + 1] = l_tot;
+    }
+  }
+}
+
+// Combines the partition partials of every (sequence, q-head) whose sequence spans more than
+// one partition, in partition order (deterministic): m = max m_s, w_s = 2^(m_s - m),
+// out = sum w_s o_s / sum w_s l_s.
+template <int D, typename Tag>
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
+  constexpr int PER = D / 64;  // d-values per thread
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int ctx = seq_len(a, b);
+  const int nsplit = (ctx + a.split_tokens - 1) / a.split_tokens;
+  if (nsplit <= 1) return;
+  const int64_t slot0 = (int64_t(b) * a.hq + h) * a.max_splits;
+  float m = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) m = fmaxf(m, a.part_ml[2 * (slot0 + s)]);
+  float acc[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) acc[j] = 0.f;
+  float l = 0.f;
+  const int d0 = threadIdx.x * PER;
+  if (m != -INFINITY) {
+    for (int s = 0; s < nsplit; ++s) {
+      const float ms = a.part_ml[2 * (slot0 + s)];
+      const float w = ms == -INFINITY ? 0.f : fast_exp2(ms - m);
+      l += w * a.part_ml[2 * (slot0 + s) + 1];
+      const float* src = a.part_o + (slot0 + s) * D + d0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) acc[j] += w * src[j];
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  uint16_t* orow = a.out + (int64_t(b) * a.hq + h) * D + d0;
+#pragma unroll
+  for (int j = 0; j < PER; j += 2) {
+    *reinterpret_cast<uint32_t*>(orow + j) = pack2(acc[j] * inv, acc[j + 1] * inv, Tag{});
+  }
+}
+
+template <int D, typename Tag, int WPB>
+int launch_mfma(const DecodeArgs& a, int batch, hipStream_t stream) {
+  hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB>), dim3(a.hkv / WPB, a.max_splits, batch),
+                     dim3(64 * WPB), 0, stream, a);
+  return check_launch("ti_gqa_decode_paged (mfma)");
+}
+
+template <int D, typename Tag>
+int launch_decode(const DecodeArgs& a, int batch, int variant, hipStream_t stream) {
+  (void)variant;  // the scalar variant is dispatched by launch_decode_scalar
+  int rc;
+  if (a.hkv % 4 == 0) {
+    rc = launch_mfma<D, Tag, 4>(a, batch, stream);
+  } else if (a.hkv % 2 == 0) {
+    rc = launch_mfma<D, Tag, 2>(a, batch, stream);
+  } else {
+    rc = launch_mfma<D, Tag, 1>(a, batch, stream);
+  }
+  if (rc != TI_OK) return rc;
+  if (a.max_splits > 1) {
+    hipLaunchKernelGGL((decode_merge_kernel<D, Tag>), dim3(a.hq, batch), dim3(64), 0, stream, a);
+    return check_launch("ti_gqa_decode_paged (merge)");
+  }
+  return TI_OK;
+}
+
+int64_t lcm64(int64_t x, int64_t y) {
+  int64_t p = x, q = y;
+  while (q) {
+    int64_t t = p % q;
+    p = q;
+    q = t;
+  }
+  return x / p * y;
+}
+
+int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, int32_t max_blocks,
+         int32_t split_req, int32_t* split_out, int32_t* max_splits_out, int64_t* ws_out) {
+  if (batch < 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0) {
+    return fail(TI_EINVAL, "decode: bad head counts batch=%d hq=%d hkv=%d", batch, hq, hkv);
+  }
+  if (hq / hkv > 16) {
+    return fail(TI_EUNSUPPORTED, "decode: query group %d exceeds the 16-row MFMA tile", hq / hkv);
+  }
+  if (D != 128 && D != 256) {
+    return fail(TI_EUNSUPPORTED, "decode: head_dim %d not built (128, 256)", D);
+  }
+  if (page_size <= 0 || page_size % 16 != 0) {
+    return fail(TI_EUNSUPPORTED, "decode: page_size %d is not a positive multiple of 16",
+                page_size);
+  }
+  if (max_blocks < 0) return fail(TI_EINVAL, "decode: max_blocks_per_seq %d < 0", max_blocks);
+  const int64_t bound = int64_t(max_blocks) * page_size;
+  if (bound > (int64_t(1) << 30)) {
+    return fail(TI_EINVAL, "decode: context bound %lld too large", (long long)bound);
+  }
+  const int64_t unit = lcm64(32, page_size);
+  int64_t split;
+  if (split_req > 0) {
+    split = split_req;
+    if (split % unit != 0 || split > kMaxSplitTokens || split / page_size > kMaxSplitPages) {
+      return fail(TI_EINVAL,
+                  "decode: split_tokens %d must be a multiple of %lld and <= %d tokens / %d pages",
+                  split_req, (long long)unit, kMaxSplitTokens, kMaxSplitPages);
+    }
+  } else {
+    // Aim for >= 8 waves per CU over the whole grid without cutting partitions below 256 tokens.
+    const int64_t target_waves = int64_t(8) * device_cu_count();
+    split = 2048;
+    while (split > 256 && int64_t(batch) * hkv * ceil_div(bound, split) < target_waves) split /= 2;
+    split = ceil_div(split, unit) * unit;
+    while (split / page_size > kMaxSplitPages) split -= unit;
+    if (split <= 0) split = unit;
+  }
+  int64_t max_splits = bound > 0 ? ceil_div(bound, split) : 1;
+  if (max_splits > 65535) return fail(TI_EINVAL, "decode: %lld partitions", (long long)max_splits);
+  *split_out = int32_t(split);
+  *max_splits_out = int32_t(max_splits);
+  *ws_out = max_splits > 1 ? int64_t(batch) * hq * max_splits * (D + 2) * 4 : 0;
+  return TI_OK;
+}
+
+}  // namespace
+}  // namespace ti
+
+extern "C" int ti_gqa_decode_plan(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                  int32_t head_dim, int32_t page_size, int32_t max_blocks_per_seq,
+                                  int32_t split_tokens, int32_t* split_tokens_out,
+                                  int32_t* max_splits_out, int64_t* workspace_bytes_out) {
+  if (!split_tokens_out || !max_splits_out || !workspace_bytes_out) {
+    return ti::fail(TI_EINVAL, "ti_gqa_decode_plan: null output pointer");
+  }
+  return ti::plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq,
+                  split_tokens, split_tokens_out, max_splits_out, workspace_bytes_out);
+}
+
+extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                   const void* k_cache, const void* v_cache,
+                                   const int32_t* block_table, int64_t block_table_stride,
+                                   const int32_t* seqlen, void* out, void* workspace,
+                                   int64_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+                                   int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                   int64_t num_blocks, int32_t max_blocks_per_seq,
+                                   int32_t split_tokens, int32_t variant, int32_t dtype,
+                                   void* stream) {
+  using namespace ti;
+  if (dtype != TI_DTYPE_BF16 && dtype != TI_DTYPE_F16) {
+    return fail(TI_EUNSUPPORTED, "ti_gqa_decode_paged: dtype code %d is not bf16/fp16", dtype);
+  }
+  if (variant != TI_DECODE_AUTO && variant != TI_DECODE_MFMA && variant != TI_DECODE_SCALAR) {
+    return fail(TI_EINVAL, "ti_gqa_decode_paged: unknown variant %d", variant);
+  }
+  int32_t split = 0, max_splits = 0;
+  int64_t ws_need = 0;
+  int rc = plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq,
+                split_tokens, &split, &max_splits, &ws_need);
+  if (rc != TI_OK) return rc;
+  if (batch == 0) return TI_OK;
+  if (!q || !k_cache || !v_cache || !block_table || !seqlen || !out) {
+    return fail(TI_EINVAL, "ti_gqa_decode_paged: null pointer");
+  }
+  if (num_blocks < 0 || block_table_stride < max_blocks_per_seq) {
+    return fail(TI_EINVAL, "ti_gqa_decode_paged: num_blocks=%lld, block_table_stride=%lld < %d",
+                (long long)num_blocks, (long long)block_table_stride, max_blocks_per_seq);
+  }
+  if (q_stride_h % 8 != 0 || q_stride_b % 8 != 0 || q_stride_h < head_dim ||
+      (reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(k_cache) & 15) ||
+      (reinterpret_cast<uintptr_t>(v_cache) & 15) || (reinterpret_cast<uintptr_t>(out) & 15)) {
+    return fail(TI_EINVAL, "ti_gqa_decode_paged: q/cache/out must be 16-byte aligned rows");
+  }
+  if (ws_need > 0 && (workspace == nullptr || workspace_bytes < ws_need ||
+                      (reinterpret_cast<uintptr_t>(workspace) & 15))) {
+    return fail(TI_EINVAL, "ti_gqa_decode_paged: workspace of %lld bytes (16-byte aligned) needed",
+                (long long)ws_need);
+  }
+  DecodeArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  a.k_cache = static_cast<const uint16_t*>(k_cache);
+  a.v_cache = static_cast<const uint16_t*>(v_cache);
+  a.row_stride = int64_t(num_kv_heads) * head_dim;
+  a.page_stride = a.row_stride * page_size;
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.seqlen = seqlen;
+  a.out = static_cast<uint16_t*>(out);
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = a.part_o ? a.part_o + int64_t(batch) * num_q_heads * max_splits * head_dim : nullptr;
+  a.num_blocks = num_blocks;
+  a.hq = num_q_heads;
+  a.hkv = num_kv_heads;
+  a.group = num_q_heads / num_kv_heads;
+  a.page_size = page_size;
+  a.max_blocks = max_blocks_per_seq;
+  a.max_splits = max_splits;
+  a.split_tokens = split;
+  a.scale_log2 = float(1.4426950408889634 / sqrt(double(head_dim)));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool bf16 = dtype == TI_DTYPE_BF16;
+  if (variant == TI_DECODE_SCALAR) {
+    rc = launch_decode_scalar(a, batch, bf16, head_dim, s);
+    if (rc != TI_OK) return rc;
+    if (max_splits > 1) {
+      if (head_dim == 256) {
+        if (bf16) hipLaunchKernelGGL((decode_merge_kernel<256, Bf16>), dim3(num_q_heads, batch), dim3(64), 0, s, a);
+        else hipLaunchKernelGGL((decode_merge_kernel<256, F16>), dim3(num_q_heads, batch), dim3(64), 0, s, a);
+      } else {
+        if (bf16) hipLaunchKernelGGL((decode_merge_kernel<128, Bf16>), dim3(num_q_heads, batch), dim3(64), 0, s, a);
+        else hipLaunchKernelGGL((decode_merge_kernel<128, F16>), dim3(num_q_heads, batch), dim3(64), 0, s, a);
+      }
+      return check_launch("ti_gqa_decode_paged (merge)");
+    }
+    return TI_OK;
+  }
+  if (head_dim == 256) {
+    return bf16 ? launch_decode<256, Bf16>(a, batch, variant, s)
+                : launch_decode<256, F16>(a, batch, variant, s);
+  }
+  return bf16 ? launch_decode<128, Bf16>(a, batch, variant, s)
+              : launch_decode<128, F16>(a, batch, variant, s);
+}

@@ -1,0 +1,136 @@
+"""Paged GQA decode attention — drop-in for tileInfer's ``kernels/gqa_decode_paged.py``.
+
+``gqa_decode_paged_fn(q, k_cache, v_cache, block_table, seqlen_kv, page_size=16)`` keeps the
+reference's positional signature, defaults and result (kernels/gqa_decode_paged.py:392-437): one
+query token per sequence attends over ``seqlen_kv[b]`` cached tokens gathered through
+``block_table[b]``, with query head ``h`` reading KV head ``h // (H_q // H_kv)``; the return value
+is a new ``[B, H_q, D]`` tensor in ``q``'s dtype.
+
+The work runs in libtileinfer_amd.so (``ti_gqa_decode_paged``): a split-K partial kernel on the
+gfx950 matrix cores plus a fixed-order merge, enqueued on the current stream. The output and the
+split-K workspace come from torch's caching allocator, so the call is graph-capture safe. Unlike
+the reference wrapper it never pads the block table (kernels/gqa_decode_paged.py:421-430): any
+table width works, entries at or beyond ``ceil(seqlen/page_size)`` are never read, and block ids
+outside the cache at positions ``< seqlen`` are treated as absent instead of being read.
+
+As in the reference, the caches are treated as flat ``[num_rows, H_kv, D]`` token rows grouped in
+pages of ``page_size`` rows (kernels/gqa_decode_paged.py:403-406), so ``page_size`` need not equal
+``k_cache.shape[1]`` as long as it tiles the rows; this build requires it to be a multiple of 16.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _lib
+
+__all__ = ["gqa_decode_paged_fn", "decode_plan"]
+
+_VARIANTS = {"auto": _lib.TI_DECODE_AUTO, "mfma": _lib.TI_DECODE_MFMA,
+             "scalar": _lib.TI_DECODE_SCALAR}
+
+
+def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
+                max_blocks_per_seq: int, split_tokens: int | None = None) -> tuple[int, int, int]:
+    """(split_tokens, max_splits, workspace_bytes) the library uses for these host-known bounds."""
+    lib = _lib.load()
+    s, m, w = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    _lib.check(lib.ti_gqa_decode_plan(batch, num_q_heads, num_kv_heads, head_dim, page_size,
+                                      max_blocks_per_seq, int(split_tokens or 0),
+                                      ctypes.byref(s), ctypes.byref(m), ctypes.byref(w)))
+    return s.value, m.value, w.value
+
+
+def _aligned_rows(t: torch.Tensor) -> bool:
+    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+            and all(s % 8 == 0 for s in t.stride()[:-1]))
+
+
+def gqa_decode_paged_fn(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seqlen_kv: torch.Tensor,
+    page_size: int = 16,
+    *,
+    out: torch.Tensor | None = None,
+    split_tokens: int | None = None,
+    variant: str = "auto",
+) -> torch.Tensor:
+    """Single-query paged GQA attention.
+
+    Args (kernels/gqa_decode_paged.py:392-399, shapes at model/qwen_36.py:1071-1079):
+        q: [B, H_q, D]
+        k_cache, v_cache: [num_blocks, block_size, H_kv, D], contiguous
+        block_table: [B, W] int32 physical page ids (-1 padding allowed past each sequence)
+        seqlen_kv: [B] int32 context lengths (including the token appended this step)
+        page_size: tokens per page of the flattened cache
+        out: keyword-only preallocated [B, H_q, D] output (contiguous, q's dtype)
+        split_tokens: keyword-only split-K partition length (None: the library's choice)
+        variant: keyword-only "auto" | "mfma" | "scalar" kernel choice
+    Returns:
+        [B, H_q, D] tensor in q's dtype.
+    """
+    if q.dim() != 3:
+        raise ValueError(f"q must be [B, H_q, D], got {tuple(q.shape)}")
+    b, h_q, d = q.shape
+    if k_cache.dim() != 4:
+        raise ValueError(f"k_cache must be [num_blocks, block_size, H_kv, D], got {tuple(k_cache.shape)}")
+    if v_cache.shape != k_cache.shape:
+        raise ValueError(f"v_cache shape {tuple(v_cache.shape)} != k_cache {tuple(k_cache.shape)}")
+    nb, bs, h_kv, d2 = k_cache.shape
+    if d2 != d:
+        raise ValueError(f"head_dim mismatch: q {d}, cache {d2}")
+    if h_kv <= 0 or h_q % h_kv != 0:
+        raise ValueError(f"H_q={h_q} is not a multiple of H_kv={h_kv}")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache and v_cache must be contiguous (a copy of the cache is never made)")
+    dt = q.dtype
+    if not (k_cache.dtype == v_cache.dtype == dt):
+        raise TypeError(f"dtype mismatch: q {dt}, k_cache {k_cache.dtype}, v_cache {v_cache.dtype}")
+    code = _lib.dtype_code(dt)
+    if block_table.dtype != torch.int32 or seqlen_kv.dtype != torch.int32:
+        raise TypeError(f"block_table/seqlen_kv must be int32, got {block_table.dtype}/{seqlen_kv.dtype}")
+    if block_table.dim() != 2 or block_table.shape[0] != b:
+        raise ValueError(f"block_table must be [{b}, W], got {tuple(block_table.shape)}")
+    if seqlen_kv.dim() != 1 or seqlen_kv.shape[0] != b:
+        raise ValueError(f"seqlen_kv must be [{b}], got {tuple(seqlen_kv.shape)}")
+    page_size = int(page_size)
+    rows = nb * bs
+    if page_size <= 0 or rows % page_size != 0:
+        raise ValueError(f"page_size {page_size} does not tile the cache's {rows} rows")
+    if variant not in _VARIANTS:
+        raise ValueError(f"variant must be one of {sorted(_VARIANTS)}, got {variant!r}")
+    dev = q.device
+    if dev.type != "cuda":
+        raise ValueError("gqa_decode_paged_fn runs on the GPU; q is on " + str(dev))
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache), ("block_table", block_table),
+                    ("seqlen_kv", seqlen_kv)):
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, q on {dev}")
+    if block_table.stride(-1) != 1:
+        block_table = block_table.contiguous()
+    if not seqlen_kv.is_contiguous():
+        seqlen_kv = seqlen_kv.contiguous()
+    if not _aligned_rows(q):
+        q = q.contiguous()
+    if out is None:
+        out = torch.empty((b, h_q, d), dtype=dt, device=dev)
+    elif (out.shape != (b, h_q, d) or out.dtype != dt or out.device != dev
+          or not out.is_contiguous()):
+        raise ValueError("out must be a contiguous [B, H_q, D] tensor of q's dtype and device")
+    if b == 0:
+        return out
+    width = block_table.shape[1]
+    _, _, ws_bytes = decode_plan(b, h_q, h_kv, d, page_size, width, split_tokens)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    lib = _lib.load()
+    _lib.check(lib.ti_gqa_decode_paged(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+        block_table.data_ptr(), block_table.stride(0) if width > 0 else 0, seqlen_kv.data_ptr(),
+        out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes,
+        b, h_q, h_kv, d, page_size, rows // page_size, width, int(split_tokens or 0),
+        _VARIANTS[variant], code, _lib.stream_handle(dev)))
+    return out

@@ -1,0 +1,205 @@
+"""Seeded synthetic inputs of the paged KV-cache benchmark configurations.
+
+Shapes follow the model the reference serves (24 query heads, 4 KV heads, head_dim 256, block
+size 16, bf16). Every builder takes a ``torch.Generator`` seed and a device; values are drawn on
+that device, so CPU-generated inputs copied to the GPU are identical to what a CPU checker sees.
+
+A decode step of one attention layer is: append the new token of each sequence through
+``slot_mapping`` (its position is ``ctx - 1``), then decode with ``seqlen = ctx``
+(model/qwen_36.py:1018 then 1074).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+HQ, HKV, HEAD_DIM, BLOCK = 24, 4, 256, 16
+
+
+@dataclass
+class PagedStep:
+    """One attention layer's inputs for append + decode."""
+    q: torch.Tensor             # [B, HQ, D]
+    k_new: torch.Tensor         # [N, HKV, D]
+    v_new: torch.Tensor         # [N, HKV, D]
+    slot_mapping: torch.Tensor  # [N] int32
+    block_table: torch.Tensor   # [B, W] int32, -1 padded
+    seqlen: torch.Tensor        # [B] int32 (after the append)
+    k_cache: torch.Tensor       # [num_blocks, BLOCK, HKV, D]
+    v_cache: torch.Tensor
+    page_size: int = BLOCK
+    meta: dict = field(default_factory=dict)
+
+    def append_bytes(self) -> int:
+        return append_bytes(self.slot_mapping, self.k_new.shape[1] * self.k_new.shape[2],
+                            self.k_new.element_size())
+
+    def decode_bytes(self) -> int:
+        return decode_bytes(self.seqlen.tolist(), self.q.shape[1], self.k_cache.shape[2],
+                            self.q.shape[2], self.page_size, self.q.element_size())
+
+
+def append_bytes(slot_mapping: torch.Tensor, row_elems: int, elem: int = 2) -> int:
+    """Algorithmic bytes of an append: read + write K and V rows of valid slots, read the slots."""
+    n_valid = int((slot_mapping >= 0).sum())
+    return 4 * row_elems * elem * n_valid + 4 * slot_mapping.numel()
+
+
+def decode_bytes(ctx: list[int], hq: int = HQ, hkv: int = HKV, d: int = HEAD_DIM,
+                 page_size: int = BLOCK, elem: int = 2) -> int:
+    """Algorithmic bytes of a decode: K+V rows, q in and out, block-table entries, seqlens."""
+    tot = sum(ctx)
+    pages = sum((c + page_size - 1) // page_size for c in ctx)
+    return 2 * hkv * d * elem * tot + 2 * hq * d * elem * len(ctx) + 4 * pages + 4 * len(ctx)
+
+
+def decode_flops(ctx: list[int], hq: int = HQ, d: int = HEAD_DIM) -> int:
+    return 4 * hq * d * sum(ctx)
+
+
+def _randn(shape, gen, device, dtype, scale=1.0):
+    x = torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
+    if scale != 1.0:
+        x.mul_(scale)
+    return x.to(dtype)
+
+
+def tables_from_pool(ctx: list[int], pool: int, gen: torch.Generator, device,
+                     width: int | None = None) -> torch.Tensor:
+    """Disjoint random physical blocks per sequence, drawn from randperm(pool); -1 padded."""
+    need = [(c + BLOCK - 1) // BLOCK for c in ctx]
+    if sum(need) > pool:
+        raise ValueError(f"pool {pool} < {sum(need)} blocks needed")
+    perm = torch.randperm(pool, generator=gen, device=device).to(torch.int32)
+    w = max(need) if width is None else width
+    table = torch.full((len(ctx), w), -1, dtype=torch.int32, device=device)
+    off = 0
+    for i, n in enumerate(need):
+        table[i, :n] = perm[off:off + n]
+        off += n
+    return table
+
+
+def decode_slots(table: torch.Tensor, ctx: list[int]) -> torch.Tensor:
+    """Slot of the token at position ctx-1 of every sequence (-1 for an empty sequence)."""
+    pos = torch.tensor([max(c - 1, 0) for c in ctx], dtype=torch.int64)
+    rows = table.cpu()[torch.arange(len(ctx)), pos // BLOCK].long()
+    slots = rows * BLOCK + pos % BLOCK
+    slots[torch.tensor([c <= 0 for c in ctx], dtype=torch.bool)] = -1
+    return slots.to(torch.int32).to(table.device)
+
+
+def make_step(ctx: list[int], pool: int, seed: int, device="cpu", dtype=torch.bfloat16,
+              value_scale: float = 1.0, width: int | None = None, hq: int = HQ, hkv: int = HKV,
+              d: int = HEAD_DIM) -> PagedStep:
+    gen = torch.Generator(device=device).manual_seed(seed)
+    table = tables_from_pool(ctx, pool, gen, device, width)
+    k_cache = _randn((pool, BLOCK, hkv, d), gen, device, dtype, value_scale)
+    v_cache = _randn((pool, BLOCK, hkv, d), gen, device, dtype, value_scale)
+    b = len(ctx)
+    q = _randn((b, hq, d), gen, device, dtype, value_scale)
+    k_new = _randn((b, hkv, d), gen, device, dtype, value_scale)
+    v_new = _randn((b, hkv, d), gen, device, dtype, value_scale)
+    return PagedStep(q=q, k_new=k_new, v_new=v_new, slot_mapping=decode_slots(table, ctx),
+                     block_table=table, seqlen=torch.tensor(ctx, dtype=torch.int32, device=device),
+                     k_cache=k_cache, v_cache=v_cache, meta={"seed": seed, "ctx": list(ctx)})
+
+
+def config1(seed: int = 1001, device="cpu", ctx: int = 512) -> PagedStep:
+    """One sequence, 64-block pool, table = randperm(64), values N(0,1)/sqrt(256)."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    perm = torch.randperm(64, generator=gen, device=device).to(torch.int32)
+    s = 1.0 / math.sqrt(HEAD_DIM)
+    k_cache = _randn((64, BLOCK, HKV, HEAD_DIM), gen, device, torch.bfloat16, s)
+    v_cache = _randn((64, BLOCK, HKV, HEAD_DIM), gen, device, torch.bfloat16, s)
+    q = _randn((1, HQ, HEAD_DIM), gen, device, torch.bfloat16, s)
+    k_new = _randn((1, HKV, HEAD_DIM), gen, device, torch.bfloat16, s)
+    v_new = _randn((1, HKV, HEAD_DIM), gen, device, torch.bfloat16, s)
+    table = perm.view(1, 64)
+    return PagedStep(q=q, k_new=k_new, v_new=v_new, slot_mapping=decode_slots(table, [ctx]),
+                     block_table=table, seqlen=torch.tensor([ctx], dtype=torch.int32, device=device),
+                     k_cache=k_cache, v_cache=v_cache, meta={"seed": seed, "ctx": [ctx]})
+
+
+def config2(seed: int = 1002, device="cpu", batch: int = 16, lo: int = 512,
+            hi: int = 8192) -> PagedStep:
+    """Batch 16, ctx ~ U[512, 8192], pool 1.25x the blocks needed, values N(0,1)."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    ctx = torch.randint(lo, hi + 1, (batch,), generator=gen).tolist()
+    need = sum((c + BLOCK - 1) // BLOCK for c in ctx)
+    return make_step(ctx, math.ceil(1.25 * need), seed, device)
+
+
+def config3(seed: int = 1003, device="cpu", batch: int = 64, ctx: int = 32768) -> PagedStep:
+    """One layer of batch 64 x 32k context; tables are one randperm of the pool split per sequence."""
+    need = batch * ((ctx + BLOCK - 1) // BLOCK)
+    return make_step([ctx] * batch, need, seed, device)
+
+
+def config4(seed: int = 1004, device="cpu", chunk: int = 2048, batch: int = 32, lo: int = 1024,
+            hi: int = 16384):
+    """Mixed step: a 2048-token prefill chunk over 128 non-contiguous blocks + 32 decode tokens.
+
+    Returns (step, chunk_slots): ``step`` is the decode batch with its 32 appended tokens;
+    ``chunk_slots``/``step.meta['chunk_k']``/``['chunk_v']`` are the prefill chunk's append.
+    """
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    ctx = torch.randint(lo, hi + 1, (batch,), generator=gen).tolist()
+    need = sum((c + BLOCK - 1) // BLOCK for c in ctx)
+    chunk_blocks = chunk // BLOCK
+    pool = math.ceil(1.25 * (need + chunk_blocks))
+    step = make_step(ctx, pool, seed, device)
+    used = set(step.block_table[step.block_table >= 0].cpu().tolist())
+    free = [i for i in range(pool) if i not in used]
+    g2 = torch.Generator(device="cpu").manual_seed(seed + 1)
+    pick = torch.randperm(len(free), generator=g2)[:chunk_blocks].tolist()
+    blocks = torch.tensor([free[i] for i in pick], dtype=torch.int64)
+    pos = torch.arange(chunk)
+    chunk_slots = (blocks[pos // BLOCK] * BLOCK + pos % BLOCK).to(torch.int32).to(device)
+    gd = torch.Generator(device=device).manual_seed(seed + 2)
+    step.meta["chunk_k"] = _randn((chunk, HKV, HEAD_DIM), gd, device, torch.bfloat16)
+    step.meta["chunk_v"] = _randn((chunk, HKV, HEAD_DIM), gd, device, torch.bfloat16)
+    step.meta["chunk_blocks"] = blocks.tolist()
+    return step, chunk_slots
+
+
+def config5(seed: int = 1005, device="cpu", batch: int = 128, prefix: int = 8192,
+            suffix: int = 512, shared: bool = True) -> PagedStep:
+    """128 sequences whose tables alias one 8192-token prefix (512 blocks) + 512 own tokens.
+
+    ``shared=False`` builds the same logical contents with every sequence holding a private copy
+    of the prefix blocks (same values, different physical ids), for the shared-vs-private check.
+    """
+    pb, sb = prefix // BLOCK, suffix // BLOCK
+    gen = torch.Generator(device=device).manual_seed(seed)
+    pool_shared = pb + batch * sb
+    pool = pool_shared if shared else batch * (pb + sb)
+    kp = _randn((pb, BLOCK, HKV, HEAD_DIM), gen, device, torch.bfloat16)
+    vp = _randn((pb, BLOCK, HKV, HEAD_DIM), gen, device, torch.bfloat16)
+    ks = _randn((batch * sb, BLOCK, HKV, HEAD_DIM), gen, device, torch.bfloat16)
+    vs = _randn((batch * sb, BLOCK, HKV, HEAD_DIM), gen, device, torch.bfloat16)
+    q = _randn((batch, HQ, HEAD_DIM), gen, device, torch.bfloat16)
+    k_new = _randn((batch, HKV, HEAD_DIM), gen, device, torch.bfloat16)
+    v_new = _randn((batch, HKV, HEAD_DIM), gen, device, torch.bfloat16)
+    k_cache = torch.empty((pool, BLOCK, HKV, HEAD_DIM), dtype=torch.bfloat16, device=device)
+    v_cache = torch.empty_like(k_cache)
+    table = torch.empty((batch, pb + sb), dtype=torch.int32, device=device)
+    if shared:
+        k_cache[:pb], v_cache[:pb] = kp, vp
+        k_cache[pb:], v_cache[pb:] = ks, vs
+        table[:, :pb] = torch.arange(pb, dtype=torch.int32, device=device)
+        table[:, pb:] = (pb + torch.arange(batch * sb, dtype=torch.int32, device=device)).view(batch, sb)
+    else:
+        for i in range(batch):
+            base = i * (pb + sb)
+            k_cache[base:base + pb], v_cache[base:base + pb] = kp, vp
+            k_cache[base + pb:base + pb + sb] = ks[i * sb:(i + 1) * sb]
+            v_cache[base + pb:base + pb + sb] = vs[i * sb:(i + 1) * sb]
+            table[i] = base + torch.arange(pb + sb, dtype=torch.int32, device=device)
+    ctx = [prefix + suffix] * batch
+    return PagedStep(q=q, k_new=k_new, v_new=v_new, slot_mapping=decode_slots(table, ctx),
+                     block_table=table, seqlen=torch.tensor(ctx, dtype=torch.int32, device=device),
+                     k_cache=k_cache, v_cache=v_cache,
+                     meta={"seed": seed, "ctx": ctx, "shared": shared})
