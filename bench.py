@@ -1,0 +1,272 @@
+"""Benchmark of the paged KV-cache hot path on one MI355X.
+
+Default workload: one decode step of the 16 full-attention layers of
+Qwen3.6-27B at batch 64 x 32,768 tokens of context (24 query heads, 4 KV heads, head_dim 256,
+block size 16, bf16 cache of [2, 16, 131072, 16, 4, 256] = 128 GiB, block tables = an independent
+random permutation of the 131,072 blocks per layer). A step = for every layer: append the batch's
+new tokens through slot_mapping, then paged decode over 32,768 tokens (split-K).
+
+Prints ONE JSON line. ``value`` is the algorithmic byte rate of the whole step (append + decode
+bytes of every layer / step time); ``roofline`` is the decode launch's algorithmic rate against
+8 TB/s, timed with HIP events on the launch stream; ``cpu_baseline`` is the CPU oracle (a
+restatement of the reference's torch path) timed on a sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--variant auto]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from tileinfer_amd.engine.kv_layout import allocate_kv_cache, layer_views  # noqa: E402
+from tileinfer_amd.kernels.gqa_decode_paged import decode_plan, gqa_decode_paged_fn  # noqa: E402
+from tileinfer_amd.kernels.kvcache_store import store_kvcache  # noqa: E402
+from tileinfer_amd.workloads import (BLOCK, HEAD_DIM, HKV, HQ, append_bytes,  # noqa: E402
+                                     decode_bytes, decode_flops)
+
+METRIC = "paged GQA decode achieved HBM GB/s (% of peak) + µs/layer-step; append GB/s"
+PEAK_HBM_GBPS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "decode_config3_traffic.txt"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_state(batch: int, ctx: int, layers: int, dev, seed: int):
+    """Cache slab, per-layer tables and inputs of the config-3 style decode step."""
+    blocks_per_seq = (ctx + BLOCK - 1) // BLOCK
+    nb = batch * blocks_per_seq
+    kv = allocate_kv_cache(layers, nb, BLOCK, HKV, HEAD_DIM, dev, torch.bfloat16, zero=False)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    for kvi in range(2):
+        for l in range(layers):
+            kv[kvi, l].normal_(generator=gen)
+    tables, slots = [], []
+    pos = ctx - 1
+    for l in range(layers):
+        t = torch.randperm(nb, generator=gen, device=dev).to(torch.int32).view(batch, blocks_per_seq)
+        tables.append(t)
+        slots.append((t[:, pos // BLOCK].long() * BLOCK + pos % BLOCK).to(torch.int32))
+    seqlen = torch.full((batch,), ctx, dtype=torch.int32, device=dev)
+    q = torch.randn((layers, batch, HQ, HEAD_DIM), generator=gen, device=dev).to(torch.bfloat16)
+    k_new = torch.randn((layers, batch, HKV, HEAD_DIM), generator=gen, device=dev).to(torch.bfloat16)
+    v_new = torch.randn((layers, batch, HKV, HEAD_DIM), generator=gen, device=dev).to(torch.bfloat16)
+    return kv, tables, slots, seqlen, q, k_new, v_new
+
+
+def read_traffic():
+    """Per-launch HBM bytes of the decode kernels from the committed rocprofv3 --pmc summary."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", TRAFFIC_FILE.read_text(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(kv, tables, seqlen, q, k_new, v_new, budget_s: float = 12.0):
+    """Time the CPU oracle (append + decode of the reference recipe) on a sample of layer 0."""
+    from oracle.ref_torch import ref_gqa_decode_paged, ref_store_kvcache
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    batch = seqlen.shape[0]
+    ctx = int(seqlen[0])
+
+    def sample(n):
+        t = tables[0][:n].cpu()
+        pages = t.reshape(-1).long()
+        kc = kv[0, 0][pages.to(kv.device)].cpu()
+        vc = kv[1, 0][pages.to(kv.device)].cpu()
+        local = torch.arange(pages.numel(), dtype=torch.int32).view(n, -1)
+        pos = ctx - 1
+        sl = (local[:, pos // BLOCK].long() * BLOCK + pos % BLOCK).to(torch.int32)
+        return (q[0, :n].cpu(), k_new[0, :n].cpu(), v_new[0, :n].cpu(), sl, local,
+                seqlen[:n].cpu(), kc, vc)
+
+    def run(args):
+        qq, kn, vn, sl, tb, sq, kc, vc = args
+        t0 = time.perf_counter()
+        ref_store_kvcache(kn, vn, kc.view(-1, HKV * HEAD_DIM), vc.view(-1, HKV * HEAD_DIM), sl)
+        ref_gqa_decode_paged(qq, kc, vc, tb, sq, BLOCK)
+        return time.perf_counter() - t0
+
+    one = sample(1)
+    run(one)  # warm-up
+    per_seq = run(one)
+    n = max(1, min(batch, int(budget_s / 4 / max(per_seq, 1e-6))))
+    args = sample(n)
+    run(args)
+    times = [run(args) for _ in range(3)]
+    t = statistics.median(times)
+    nbytes = decode_bytes([ctx] * n) + append_bytes(args[3], HKV * HEAD_DIM)
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": (f"layer 0 of the same step, {n} of {batch} sequences x {ctx} tokens: append "
+                       f"+ decode by the CPU oracle (oracle/ref_torch.py), median of 3 after 1 "
+                       f"warm-up, {t * 1e3:.1f} ms per run"),
+            "us_per_layer_step_extrapolated": round(t / n * batch * 1e6, 1)}
+
+
+def parity_sample(kv, tables, seqlen, q, k_new, v_new, out_last, layer: int, idx=(0, 37)):
+    """Full-size checks on the run itself: appended rows bit-exact; decode of sampled sequences
+    within atol 2e-2 / rtol 1e-2 of the CPU oracle."""
+    from oracle.ref_torch import ref_gqa_decode_paged
+
+    k_rows, v_rows, _, _ = layer_views(kv, layer)
+    ctx = int(seqlen[0])
+    pos = ctx - 1
+    sl = (tables[layer][:, pos // BLOCK].long() * BLOCK + pos % BLOCK)
+    append_ok = bool(torch.equal(k_rows[sl].view(torch.int16), k_new[layer].reshape(len(sl), -1).view(torch.int16))
+                     and torch.equal(v_rows[sl].view(torch.int16), v_new[layer].reshape(len(sl), -1).view(torch.int16)))
+    worst = 0.0
+    ok = True
+    for b in idx:
+        b = b % seqlen.shape[0]
+        pages = tables[layer][b].long()
+        kc = kv[0, layer][pages].cpu()
+        vc = kv[1, layer][pages].cpu()
+        tb = torch.arange(pages.numel(), dtype=torch.int32).view(1, -1)
+        ref = ref_gqa_decode_paged(q[layer, b:b + 1].cpu(), kc, vc, tb, seqlen[b:b + 1].cpu(), BLOCK)
+        got = out_last[b:b + 1].float().cpu()
+        err = (got - ref.float()).abs()
+        worst = max(worst, err.max().item())
+        ok = ok and bool((err <= 2e-2 + 1e-2 * ref.float().abs()).all())
+    return {"append_bit_exact": append_ok, "decode_within_tol": ok,
+            "decode_max_abs_err": round(worst, 6), "sampled_sequences": list(idx), "layer": layer}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--layers", type=int, default=16)
+    ap.add_argument("--variant", default="auto", choices=["auto", "mfma", "scalar"])
+    ap.add_argument("--split-tokens", type=int, default=None)
+    ap.add_argument("--seed", type=int, default=1003)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-parity", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}): "
+              "this build has no multi-GPU path; the sharding design is described in DESIGN.md.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    b, ctx, layers = args.batch, args.ctx, args.layers
+    log(f"allocating cache: batch {b} x ctx {ctx} x {layers} layers")
+    kv, tables, slots, seqlen, q, k_new, v_new = build_state(b, ctx, layers, dev, args.seed)
+    torch.cuda.synchronize()
+    log(f"cache {kv.numel() * 2 / 2**30:.1f} GiB ready")
+    views = [layer_views(kv, l) for l in range(layers)]
+    split, max_splits, ws = decode_plan(b, HQ, HKV, HEAD_DIM, BLOCK, tables[0].shape[1],
+                                        args.split_tokens)
+
+    def step(ev=None):
+        out = None
+        for l in range(layers):
+            k_rows, v_rows, k_paged, v_paged = views[l]
+            if ev is not None:
+                ev[l][0].record()
+            store_kvcache(k_new[l], v_new[l], k_rows, v_rows, slots[l])
+            if ev is not None:
+                ev[l][1].record()
+            out = gqa_decode_paged_fn(q[l], k_paged, v_paged, tables[l], seqlen, BLOCK,
+                                      split_tokens=args.split_tokens, variant=args.variant)
+            if ev is not None:
+                ev[l][2].record()
+        return out
+
+    for i in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"warm-up done ({args.warmup} steps); timing {args.steps} steps")
+    evs = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(layers)]
+           for _ in range(args.steps)]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    out = None
+    for s in range(args.steps):
+        out = step(evs[s])
+    stop.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(stop)
+    app_ms = [e[l][0].elapsed_time(e[l][1]) for e in evs for l in range(layers)]
+    dec_ms = [e[l][1].elapsed_time(e[l][2]) for e in evs for l in range(layers)]
+    log(f"timed: {total_ms:.2f} ms total")
+
+    ms_step = total_ms / args.steps
+    a_bytes = append_bytes(slots[0], HKV * HEAD_DIM)
+    d_bytes = decode_bytes([ctx] * b)
+    step_bytes = layers * (a_bytes + d_bytes)
+    dec_avg_us = statistics.mean(dec_ms) * 1e3
+    app_avg_us = statistics.mean(app_ms) * 1e3
+    dec_gbps = d_bytes / (dec_avg_us * 1e-6) / 1e9
+    traffic = read_traffic()
+
+    result = {
+        "metric": METRIC,
+        "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) K/V/q, random block permutations; resident in HBM",
+        "config": {
+            "workload": (f"config3: decode step of {layers} full-attention layers, batch {b} x "
+                         f"context {ctx}, 24Q/4KV heads, head_dim 256, block 16, bf16; per layer "
+                         f"append {b} tokens then split-K paged decode"),
+            "batch": b, "ctx": ctx, "layers": layers, "split_tokens": split,
+            "max_splits": max_splits, "variant": args.variant,
+        },
+        "us_per_layer_step": round(ms_step * 1e3 / layers, 2),
+        "decode_us_per_layer": round(dec_avg_us, 2),
+        "append_us_per_layer": round(app_avg_us, 2),
+        "decode_GBps_algorithmic": round(dec_gbps, 1),
+        "decode_pct_of_peak_hbm": round(100 * dec_gbps / PEAK_HBM_GBPS, 2),
+        "decode_TFLOPs": round(decode_flops([ctx] * b) / (dec_avg_us * 1e-6) / 1e12, 2),
+        "append_GBps_algorithmic": round(a_bytes / (app_avg_us * 1e-6) / 1e9, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(dec_gbps, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(dec_gbps / PEAK_HBM_GBPS, 4),
+            "traffic": traffic,
+            "kernel": "decode launch (split-K partial + merge), one layer",
+            "algorithmic_bytes_per_launch": d_bytes,
+        },
+    }
+    if not args.no_parity:
+        log("full-size parity sample")
+        result["parity"] = parity_sample(kv, tables, seqlen, q, k_new, v_new, out, layers - 1)
+    if not args.no_cpu_baseline:
+        log("CPU baseline (oracle) on a sample")
+        result["cpu_baseline"] = cpu_baseline(kv, tables, seqlen, q, k_new, v_new)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,102 @@
+"""The C-ABI library loads, exports every symbol include/tileinfer_amd.h declares, and rejects bad
+arguments before touching a device (CPU only: no kernel is launched here)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from tileinfer_amd import _lib
+from tileinfer_amd.kernels.gqa_decode_paged import gqa_decode_paged_fn
+from tileinfer_amd.kernels.kvcache_store import store_kvcache
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "tileinfer_amd.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(ti_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert names == sorted(_lib.SIGNATURES), "ctypes table out of sync with the header"
+    for name in names:
+        assert hasattr(lib, name), f"{name} not exported"
+    assert lib.ti_abi_version() == _lib.ABI_VERSION
+
+
+def test_header_codes_match_binding():
+    text = HEADER.read_text()
+    for name in ("TI_OK", "TI_EINVAL", "TI_ELAUNCH", "TI_EUNSUPPORTED", "TI_DTYPE_BF16",
+                 "TI_DTYPE_F16", "TI_DECODE_AUTO", "TI_DECODE_MFMA", "TI_DECODE_SCALAR"):
+        m = re.search(rf"#define {name} (\d+)", text)
+        assert m and int(m.group(1)) == getattr(_lib, name), name
+
+
+def _plan(*args):
+    lib = _lib.load()
+    s, m, w = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    rc = lib.ti_gqa_decode_plan(*args, ctypes.byref(s), ctypes.byref(m), ctypes.byref(w))
+    return rc, s.value, m.value, w.value
+
+
+def test_decode_plan_sizes():
+    # Config 3 with 2048-token partitions: 16 partitions, fp32 partials (o + m,l) per q-head.
+    rc, split, ms, ws = _plan(64, 24, 4, 256, 16, 2048, 2048)
+    assert (rc, split, ms, ws) == (0, 2048, 16, 64 * 24 * 16 * (256 + 2) * 4)
+    # A bound that fits one partition needs no workspace.
+    assert _plan(8, 24, 4, 256, 16, 64, 2048)[1:] == (2048, 1, 0)
+
+
+@pytest.mark.parametrize("args,code", [
+    ((4, 24, 4, 256, 8, 100, 2048), _lib.TI_EUNSUPPORTED),    # page size not a multiple of 16
+    ((4, 64, 2, 256, 16, 100, 2048), _lib.TI_EUNSUPPORTED),   # group of 32 > 16-row tile
+    ((4, 24, 4, 96, 16, 100, 2048), _lib.TI_EUNSUPPORTED),    # head_dim not built
+    ((4, 24, 4, 256, 16, 100, 100), _lib.TI_EINVAL),          # split not a multiple of 32
+    ((4, 24, 4, 256, 16, 100, 16384), _lib.TI_EINVAL),        # split above the maximum
+    ((4, 25, 4, 256, 16, 100, 2048), _lib.TI_EINVAL),         # Hq not a multiple of Hkv
+])
+def test_decode_plan_rejects(args, code):
+    rc = _plan(*args)[0]
+    assert rc == code
+    assert _lib.load().ti_last_error().decode()
+
+
+def test_append_argument_errors_without_device():
+    lib = _lib.load()
+    assert lib.ti_kv_append(None, None, 8, 8, None, None, 8, None, 0, 8, 10, 0, None) == _lib.TI_OK
+    rc = lib.ti_kv_append(None, None, 8, 8, None, None, 8, None, 4, 8, 10, 7, None)
+    assert rc == _lib.TI_EUNSUPPORTED and b"dtype" in lib.ti_last_error()
+    rc = lib.ti_kv_append(None, None, 8, 8, None, None, 8, None, 4, 8, 10, 0, None)
+    assert rc == _lib.TI_EINVAL and b"null" in lib.ti_last_error()
+    with pytest.raises(_lib.TileInferError):
+        _lib.check(rc)
+
+
+def test_python_wrappers_validate_before_launch():
+    k = torch.zeros(2, 4, 256, dtype=torch.bfloat16)
+    cache = torch.zeros(64, 1024, dtype=torch.bfloat16)
+    with pytest.raises(TypeError):
+        store_kvcache(k, k, cache, cache, torch.zeros(2, dtype=torch.int64))
+    with pytest.raises(ValueError):
+        store_kvcache(k, k, cache[:, :512], cache[:, :512], torch.zeros(2, dtype=torch.int32))
+    with pytest.raises(ValueError, match="GPU"):
+        store_kvcache(k, k, cache, cache, torch.zeros(2, dtype=torch.int32))
+    q = torch.zeros(2, 24, 256, dtype=torch.bfloat16)
+    kc = torch.zeros(4, 16, 4, 256, dtype=torch.bfloat16)
+    bt = torch.zeros(2, 4, dtype=torch.int32)
+    sl = torch.ones(2, dtype=torch.int32)
+    with pytest.raises(TypeError):
+        gqa_decode_paged_fn(q, kc.float(), kc, bt, sl)
+    with pytest.raises(ValueError):
+        gqa_decode_paged_fn(q, kc, kc, bt, sl, page_size=24)
+    with pytest.raises(ValueError, match="GPU"):
+        gqa_decode_paged_fn(q, kc, kc, bt, sl)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="no non-HIP fallback"):
+        _lib.load(tmp_path / "absent.so")

@@ -1,0 +1,277 @@
+"""Block manager, prefix cache, sharing flow and metadata builders (CPU, pure Python).
+
+Expected block ids are derived by hand from the reference's rules: a fresh pool hands out 0, 1,
+2, ... (free list [n-1..0] popped from the end, engine/block_manager.py:33, 45), freed blocks are
+reused last-in first-out, and deallocation walks a table in reverse (engine/block_manager.py:95).
+"""
+import numpy as np
+import pytest
+import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+from tileinfer_amd.engine import (AttentionContext, BlockManager, PagedKVManager, PrefixCache,
+                                  Sequence, get_context, reset_context, set_context)
+from tileinfer_amd.engine import kv_layout as kl
+
+
+@pytest.fixture(autouse=True)
+def _bs16():
+    Sequence.block_size = 16
+    yield
+    Sequence.block_size = 16
+
+
+def seq(n, start=0):
+    return Sequence(list(range(start, start + n)))
+
+
+# ----------------------------------------------------------------------------- sequence
+
+
+def test_sequence_layout_fields():
+    s = seq(33)
+    assert len(s) == 33 and s.num_blocks == 3 and s.last_block_num_tokens == 1
+    assert s.block(2) == [32]
+    s.append_token(99)
+    assert s.num_tokens == 34 and s.last_token == 99 and s.num_prompt_tokens == 33
+    with pytest.raises(ValueError):
+        Sequence([])
+    with pytest.raises(IndexError):
+        s.block(3)
+
+
+# ----------------------------------------------------------------------------- block manager
+
+
+def test_allocation_order_and_lifo_reuse():
+    bm = BlockManager(8, 16)
+    a, b = seq(40), seq(17)
+    bm.allocate(a)
+    bm.allocate(b)
+    assert a.block_table == [0, 1, 2] and b.block_table == [3, 4]
+    assert bm.num_free_blocks == 3
+    freed = bm.deallocate(a)
+    assert freed == [2, 1, 0] and a.block_table == []
+    c = seq(48)
+    bm.allocate(c)
+    assert c.block_table == [0, 1, 2]  # last freed (0) comes back first
+
+
+def test_share_blocks_refcounts_and_release():
+    bm = BlockManager(6, 16)
+    events = []
+    bm.on_block_freed = events.append
+    a = seq(32)
+    bm.allocate(a)
+    b = seq(40)
+    bm.share_blocks(b, a.block_table[:2])
+    bm.allocate_extra(b)
+    assert b.block_table == [0, 1, 2]
+    assert [bm.blocks[i].ref_count for i in range(3)] == [2, 2, 1]
+    assert bm.deallocate(a) == [] and events == []
+    assert bm.deallocate(b) == [2, 1, 0] and events == [2, 1, 0]
+    assert bm.num_free_blocks == 6
+    with pytest.raises(ValueError):
+        bm.share_blocks(seq(1), [5])  # a free block cannot be shared
+
+
+def test_may_append_reference_trigger_and_capacity_fix():
+    bm = BlockManager(10, 16)
+    a = seq(20)                     # 2 blocks: 0, 1
+    bm.allocate(a)
+    while len(a) < 31:
+        a.append_token(0)
+        bm.may_append(a)
+    assert a.block_table == [0, 1]
+    a.append_token(0)               # len 32: the reference allocates one block ahead
+    assert bm.can_append(a)
+    bm.may_append(a)
+    assert a.block_table == [0, 1, 2]
+    b = seq(16)                     # prompt a multiple of 16: block 3
+    bm.allocate(b)
+    b.append_token(0)               # len 17: position 16 needs a second block (reference misses it)
+    bm.may_append(b)
+    assert b.block_table == [3, 4]
+    assert len(b.block_table) * 16 >= len(b)
+
+
+def test_can_append_on_exhausted_pool():
+    bm = BlockManager(1, 16)
+    a = seq(16)
+    bm.allocate(a)
+    a.append_token(0)
+    assert not bm.can_append(a)
+    with pytest.raises(RuntimeError):
+        bm.may_append(a)
+
+
+# ----------------------------------------------------------------------------- prefix cache
+
+
+def test_prefix_cache_whole_blocks_only():
+    pc = PrefixCache(4)
+    toks = list(range(10))
+    pc.add(toks, [7, 8, 9])
+    assert pc.num_entries == 2                              # boundaries at 4 and 8 tokens
+    assert pc.find_longest_prefix(toks) == ([7, 8], 8)
+    assert pc.find_longest_prefix(toks[:7]) == ([7], 4)
+    assert pc.find_longest_prefix([0, 1, 2, 99, 4]) == ([], 0)
+    pc.add(toks, [7, 8, 9])                                 # idempotent
+    assert pc.num_entries == 2
+
+
+def test_prefix_cache_position_sensitive():
+    pc = PrefixCache(2)
+    pc.add([1, 2, 3, 4], [10, 11])
+    assert pc.find_longest_prefix([3, 4, 1, 2]) == ([], 0)  # same tokens, other position
+
+
+def test_prefix_cache_eviction_invalidates_subtree():
+    pc = PrefixCache(2)
+    pc.add([1, 2, 3, 4, 5, 6], [10, 11, 12])
+    pc.add([1, 2, 7, 8], [10, 13])
+    assert pc.num_entries == 4
+    pc.evict_block(11)                 # chain [10, 11] and its child [10, 11, 12] go
+    assert pc.find_longest_prefix([1, 2, 3, 4, 5, 6]) == ([10], 2)
+    assert pc.find_longest_prefix([1, 2, 7, 8]) == ([10, 13], 4)
+    assert pc.num_entries == 2
+    pc.evict_block(10)
+    assert pc.find_longest_prefix([1, 2, 7, 8]) == ([], 0)
+    assert pc.num_entries == 0
+
+
+def test_prefix_cache_trim():
+    pc = PrefixCache(1, max_entries=2)
+    pc.add([1, 2, 3], [5, 6, 7])
+    assert pc.num_entries == 2
+
+
+# ----------------------------------------------------------------------------- sharing flow
+
+
+def test_manager_prefix_hit_shares_and_allocates_rest():
+    m = PagedKVManager(20, 16)
+    a = Sequence(list(range(40)))
+    assert m.admit(a) and a.block_table == [0, 1, 2]
+    m.finish_chunk(a, 32)                      # 32 tokens computed: 2 whole blocks recorded
+    b = Sequence(list(range(32)) + [100] * 10)
+    assert m.admit(b)
+    assert b.block_table[:2] == [0, 1] and b.num_cached_tokens == 32 and b.block_table[2] == 3
+    assert m.block_manager.blocks[0].ref_count == 2
+    m.free(a)
+    m.free(b)
+    assert m.prefix_cache.num_entries == 0     # blocks 0, 1 freed -> entries evicted
+    assert m.block_manager.num_free_blocks == 20
+
+
+def test_manager_full_prefix_match_leaves_a_token_to_prefill():
+    m = PagedKVManager(10, 16)
+    a = Sequence(list(range(32)))
+    m.admit(a)
+    m.finish_chunk(a, 32)
+    b = Sequence(list(range(32)))
+    assert m.admit(b)
+    assert b.num_cached_tokens == 16 and b.block_table[0] == 0 and b.block_table[1] != 1
+
+
+def test_manager_admission_fails_without_room():
+    m = PagedKVManager(2, 16)
+    assert not m.admit(Sequence(list(range(40))))
+    assert m.block_manager.num_free_blocks == 2
+
+
+@settings(max_examples=60, deadline=None)
+@given(st.lists(st.tuples(st.sampled_from(["admit", "decode", "free"]),
+                          st.integers(0, 5), st.integers(1, 70)), max_size=40))
+def test_manager_invariants(ops):
+    """Refcounts equal table membership, the free list is the complement of used blocks, and no
+    two live sequences write the same slot."""
+    m = PagedKVManager(24, 16)
+    live: dict[int, Sequence] = {}
+    prompts = [list(range(40)), list(range(40)) + [1, 2], list(range(17)), [9] * 50]
+    for op, k, n in ops:
+        if op == "admit" and k not in live:
+            s = Sequence((prompts[k % 4] * 3)[:n])
+            if m.admit(s):
+                m.finish_chunk(s, s.num_tokens - s.num_cached_tokens)
+                s.is_prefill = False
+                live[k] = s
+        elif op == "decode" and k in live:
+            s = live[k]
+            s.append_token(n)
+            if m.can_append(s):
+                m.append_slot(s)
+            else:
+                m.free(s)
+                del live[k]
+        elif op == "free" and k in live:
+            m.free(live.pop(k))
+        bm = m.block_manager
+        counts = {}
+        for s in live.values():
+            assert len(s.block_table) * 16 >= len(s)
+            for bid in s.block_table:
+                counts[bid] = counts.get(bid, 0) + 1
+        for bid in range(24):
+            assert bm.blocks[bid].ref_count == counts.get(bid, 0)
+        assert set(bm.free_block_ids) == set(range(24)) - set(counts)
+        slots = [s.block_table[(len(s) - 1) // 16] * 16 + (len(s) - 1) % 16 for s in live.values()]
+        assert len(slots) == len(set(slots))
+
+
+# ----------------------------------------------------------------------------- builders
+
+
+def test_slot_mappings_match_definition():
+    a, b = seq(37), seq(5)
+    a.block_table = [9, 4, 7]
+    b.block_table = [2]
+    got = kl.slot_mapping_decode([a, b], 16)
+    assert got.tolist() == [7 * 16 + 4, 2 * 16 + 4]
+    a.num_cached_tokens, a.num_scheduled_tokens = 14, 20
+    b.num_cached_tokens, b.num_scheduled_tokens = 0, 5
+    got = kl.slot_mapping_prefill([a, b], 16)
+    want = [a.block_table[p // 16] * 16 + p % 16 for p in range(14, 34)] + [32, 33, 34, 35, 36]
+    assert got.tolist() == want and got.dtype == np.int32
+    a.num_scheduled_tokens = 40
+    with pytest.raises(IndexError):
+        kl.slot_mapping_prefill([a], 16)
+
+
+def test_block_tables_and_graph_padding():
+    a, b = seq(37), seq(5)
+    a.block_table, b.block_table = [9, 4, 7], [2]
+    t = kl.block_tables([a, b])
+    assert t.tolist() == [[9, 4, 7], [2, -1, -1]]
+    slots, tables, ctx = kl.decode_metadata([a, b], 16, device="cpu", pad_to=4, width=5)
+    assert slots.tolist() == [7 * 16 + 4, 36, -1, -1]
+    assert ctx.tolist() == [37, 5, 1, 1]
+    assert tables.tolist() == [[9, 4, 7, -1, -1], [2, -1, -1, -1, -1], [-1] * 5, [-1] * 5]
+    assert tables.dtype == torch.int32 and slots.dtype == torch.int32
+
+
+def test_kv_cache_layout_views():
+    kv = kl.allocate_kv_cache(3, 5, 16, 4, 8, device="cpu")
+    assert tuple(kv.shape) == (2, 3, 5, 16, 4, 8)
+    k_rows, v_rows, k_paged, v_paged = kl.layer_views(kv, 1)
+    assert tuple(k_rows.shape) == (80, 32) and tuple(k_paged.shape) == (5, 16, 4, 8)
+    k_rows[17, 9] = 1.0                                    # the views alias the slab
+    assert float(kv[0, 1, 1, 1, 1, 1]) == 1.0
+    v_paged[0, 0, 0, 0] = 2.0
+    assert float(v_rows[0, 0]) == 2.0
+    assert kl.num_blocks_for_budget(2 * 16 * 4 * 8 * 2 * 3 * 10 + 5, 16, 4, 8, 3) == 10
+
+
+def test_attention_context_is_thread_local():
+    import threading
+    ctx = AttentionContext()
+    ctx.is_prefill = True
+    set_context(ctx)
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(get_context()))
+    t.start()
+    t.join()
+    assert seen == [None] and get_context() is ctx
+    reset_context()
+    assert get_context() is None
