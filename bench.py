@@ -44,8 +44,12 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_state(batch: int, ctx: int, layers: int, dev, seed: int):
-    """Cache slab, per-layer tables and inputs of the config-3 style decode step."""
+def build_state(batch: int, ctx: int, layers: int, dev, seed: int, sequential: bool = False):
+    """Cache slab, per-layer tables and inputs of the config-3 style decode step.
+
+    Tables are an independent random permutation of the pool per layer (config 3);
+    ``sequential`` lays every sequence's blocks out contiguously instead (a diagnostic only).
+    """
     blocks_per_seq = (ctx + BLOCK - 1) // BLOCK
     nb = batch * blocks_per_seq
     kv = allocate_kv_cache(layers, nb, BLOCK, HKV, HEAD_DIM, dev, torch.bfloat16, zero=False)
@@ -56,7 +60,9 @@ def build_state(batch: int, ctx: int, layers: int, dev, seed: int):
     tables, slots = [], []
     pos = ctx - 1
     for l in range(layers):
-        t = torch.randperm(nb, generator=gen, device=dev).to(torch.int32).view(batch, blocks_per_seq)
+        order = (torch.arange(nb, device=dev) if sequential
+                 else torch.randperm(nb, generator=gen, device=dev))
+        t = order.to(torch.int32).view(batch, blocks_per_seq)
         tables.append(t)
         slots.append((t[:, pos // BLOCK].long() * BLOCK + pos % BLOCK).to(torch.int32))
     seqlen = torch.full((batch,), ctx, dtype=torch.int32, device=dev)
@@ -145,8 +151,34 @@ def parity_sample(kv, tables, seqlen, q, k_new, v_new, out_last, layer: int, idx
             "decode_max_abs_err": round(worst, 6), "sampled_sequences": list(idx), "layer": layer}
 
 
+def calibrate(dev, gib: float = 4.0, reps: int = 5):
+    """Plain device copy and read of known size: the scale for rocprofv3 FETCH_SIZE/WRITE_SIZE
+    (bytes the counters report per byte moved) and the streaming bandwidth torch reaches."""
+    n = int(gib * 2**30) // 2
+    src = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    res = {}
+    for name, fn, nbytes in (("copy", lambda: dst.copy_(src), 4 * n),
+                             ("read_sum", lambda: src.sum(dtype=torch.float32), 2 * n)):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        res[name] = {"bytes_per_launch": nbytes, "us": round(ms * 1e3, 1),
+                     "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    print(json.dumps({"calibration": res, "copy_read_bytes": 2 * n, "copy_write_bytes": 2 * n}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
+    ap.add_argument("--calibrate", action="store_true",
+                    help="run only the copy/read calibration of known size and exit")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
@@ -158,6 +190,8 @@ def main():
     ap.add_argument("--seed", type=int, default=1003)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--sequential-tables", action="store_true",
+                    help="diagnostic: contiguous blocks per sequence instead of random permutations")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -169,9 +203,13 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate:
+        calibrate(dev)
+        return
     b, ctx, layers = args.batch, args.ctx, args.layers
     log(f"allocating cache: batch {b} x ctx {ctx} x {layers} layers")
-    kv, tables, slots, seqlen, q, k_new, v_new = build_state(b, ctx, layers, dev, args.seed)
+    kv, tables, slots, seqlen, q, k_new, v_new = build_state(b, ctx, layers, dev, args.seed,
+                                                             args.sequential_tables)
     torch.cuda.synchronize()
     log(f"cache {kv.numel() * 2 / 2**30:.1f} GiB ready")
     views = [layer_views(kv, l) for l in range(layers)]
@@ -240,6 +278,7 @@ def main():
                          f"append {b} tokens then split-K paged decode"),
             "batch": b, "ctx": ctx, "layers": layers, "split_tokens": split,
             "max_splits": max_splits, "variant": args.variant,
+            "tables": "sequential" if args.sequential_tables else "random permutation per layer",
         },
         "us_per_layer_step": round(ms_step * 1e3 / layers, 2),
         "decode_us_per_layer": round(dec_avg_us, 2),

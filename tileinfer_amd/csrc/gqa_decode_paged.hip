@@ -36,6 +36,7 @@ struct Tile {
   static constexpr int NC = D / 128;  // 16-byte d-chunks per lane per V row
   u32x4 k[2][KK];                     // [sub-tile][k-step]
   u32x4 v[2][4][NC];                  // [sub-tile][row 4g+r][chunk]
+  int rows[2];                        // tokens present in each sub-tile (uniform)
 };
 
 template <int D, typename Tag, int WPB>
@@ -48,7 +49,9 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
   __shared__ int s_bids[kMaxSplitPages];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Uniform across the wave; readfirstlane lets the compiler keep it (and every page address
+  // derived from it) in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;  // MFMA row/col index: token row of K, head of S^T/O^T, d-col of V^T
   const int g = lane >> 4;  // MFMA k-group
   const int kvh = blockIdx.x * WPB + wave;
@@ -80,8 +83,10 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
     }
   }
 
-  const int64_t lane_k = int64_t(n) * a.row_stride + kvh * D + 8 * g;
-  const int64_t lane_v = int64_t(4 * g) * a.row_stride + kvh * D + 8 * n;
+  // Byte offsets of this lane's loads inside one 16-token sub-tile of its KV head.
+  const uint32_t row_bytes = uint32_t(a.row_stride) * 2;
+  const uint32_t lane_k = uint32_t(n) * row_bytes + 16 * g;
+  const uint32_t lane_v = uint32_t(4 * g) * row_bytes + 16 * n;
 
   f32x4 o[NT];
 #pragma unroll
@@ -89,55 +94,38 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
   float m_run = -INFINITY;
   float l_run = 0.f;
 
-  // Loads one 32-token tile (two 16-token sub-tiles) at position t0 into `T`; returns a bit mask
-  // of the sub-tiles that are present (in range and with a valid block id).
-  auto load_tile = [&](Tile<D>& T, int t0) -> int {
-    int present = 0;
+  // Loads one 32-token tile (two 16-token sub-tiles) at position t0 into `T`. Every load is
+  // issued unconditionally through a buffer descriptor that spans only the sub-tile's rows that
+  // exist (in the partition and with a valid block id); rows past it read as zero with no memory
+  // access. Branch-free loads keep the compiler's count of outstanding loads exact, so waiting
+  // for one tile never waits for the tile prefetched behind it.
+  auto load_tile = [&](Tile<D>& T, int t0) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = t0 + 16 * i;
-      int bid = -1;
-      if (p < tok1) bid = __builtin_amdgcn_readfirstlane(s_bids[(p - tok0) / a.page_size]);
-      if (p < tok1 && bid >= 0 && bid < a.num_blocks) {
-        present |= 1 << i;
-        const int64_t base = int64_t(bid) * a.page_stride + int64_t(p % a.page_size) * a.row_stride;
-        const uint16_t* kb = a.k_cache + base + lane_k;
-        const uint16_t* vb = a.v_cache + base + lane_v;
+      // Past the partition end the LDS entry may be stale; `rows` is 0 there and masks it.
+      const int slot = min((p - tok0) / a.page_size, kMaxSplitPages - 1);
+      const int id = __builtin_amdgcn_readfirstlane(s_bids[slot]);
+      const bool ok = (tok1 - p > 0) && (uint32_t(id) < uint32_t(a.num_blocks32));
+      const int rows = ok ? min(tok1 - p, 16) : 0;
+      const int bid = ok ? id : 0;
+      const int64_t base =
+          int64_t(bid) * a.page_stride + int64_t(p % a.page_size) * a.row_stride + kvh * D;
+      const uint32_t nbytes = rows > 0 ? uint32_t(rows - 1) * row_bytes + D * 2 : 0u;
+      const auto rk = make_rsrc(a.k_cache + base, nbytes);
+      const auto rv = make_rsrc(a.v_cache + base, nbytes);
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) T.k[i][kk] = load16(kb + 32 * kk);
+      for (int kk = 0; kk < KK; ++kk) T.k[i][kk] = buffer_load16(rk, lane_k + 64 * kk);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < 4; ++r) {
 #pragma unroll
-          for (int c = 0; c < NC; ++c) T.v[i][r][c] = load16(vb + r * a.row_stride + 128 * c);
-        }
-      } else {
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) T.k[i][kk] = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-#pragma unroll
-          for (int c = 0; c < NC; ++c) T.v[i][r][c] = u32x4{0u, 0u, 0u, 0u};
-        }
+        for (int c = 0; c < NC; ++c) T.v[i][r][c] = buffer_load16(rv, lane_v + r * row_bytes + 256 * c);
       }
+      T.rows[i] = rows;
     }
-    return present;
   };
 
-  auto compute_tile = [&](Tile<D>& T, int t0, int present) {
-    // Rows past the partition end belong to the same page but carry no (or another
-    // partition's) token: zero their V so that 0 * garbage cannot reach the accumulators.
-    if (t0 + 32 > tok1) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (t0 + 16 * i + 4 * g + r >= tok1) {
-#pragma unroll
-            for (int c = 0; c < NC; ++c) T.v[i][r][c] = u32x4{0u, 0u, 0u, 0u};
-          }
-        }
-      }
-    }
+  auto compute_tile = [&](Tile<D>& T) {
     f32x4 s[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -150,9 +138,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int tok = t0 + 16 * i + 4 * g + r;
-        const bool ok = ((present >> i) & 1) && tok < tok1;
-        sv[4 * i + r] = ok ? s[i][r] * a.scale_log2 : -INFINITY;
+        sv[4 * i + r] = (4 * g + r < T.rows[i]) ? s[i][r] * a.scale_log2 : -INFINITY;
       }
     }
     float mx = sv[0];
@@ -202,16 +188,16 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
   const int ntiles = (tok1 - tok0 + 31) / 32;
   if (ntiles > 0) {
     Tile<D> ta, tb;
-    int pa = load_tile(ta, tok0);
+    load_tile(ta, tok0);
     int it = 0;
     for (; it + 2 <= ntiles; it += 2) {
       const int t0 = tok0 + 32 * it;
-      int pb = load_tile(tb, t0 + 32);
-      compute_tile(ta, t0, pa);
-      if (it + 2 < ntiles) pa = load_tile(ta, t0 + 64);
-      compute_tile(tb, t0 + 32, pb);
+      load_tile(tb, t0 + 32);
+      compute_tile(ta);
+      if (it + 2 < ntiles) load_tile(ta, t0 + 64);
+      compute_tile(tb);
     }
-    if (it < ntiles) compute_tile(ta, tok0 + 32 * it, pa);
+    if (it < ntiles) compute_tile(ta);
   }
 
   // Sum the per-lane partial denominators of each head (lanes n, n+16, n+32, n+48).
@@ -441,7 +427,7 @@ extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_
   a.out = static_cast<uint16_t*>(out);
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o ? a.part_o + int64_t(batch) * num_q_heads * max_splits * head_dim : nullptr;
-  a.num_blocks = num_blocks;
+  a.num_blocks32 = int32_t(num_blocks < INT32_MAX ? num_blocks : INT32_MAX);
   a.hq = num_q_heads;
   a.hkv = num_kv_heads;
   a.group = num_q_heads / num_kv_heads;

@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void decode_scalar_kernel(DecodeArgs a) {
   auto row_bid = [&](int pos) -> int {  // block id of token `pos`, -1 when absent
     if (pos >= tok1) return -1;
     const int bid = s_bids[(pos - tok0) / a.page_size];
-    return (bid >= 0 && bid < a.num_blocks) ? bid : -1;
+    return (bid >= 0 && bid < a.num_blocks32) ? bid : -1;
   };
 
   u32x4 pk[CPT], pv[CPT];
@@ -99,8 +99,8 @@ __global__ __launch_bounds__(256) void decode_scalar_kernel(DecodeArgs a) {
       if (bid >= 0) {
         const int64_t off = int64_t(bid) * a.page_stride + int64_t(pos % a.page_size) * a.row_stride +
                             int64_t(kvh) * D + 8 * col;
-        pk[k] = load16(a.k_cache + off);
-        pv[k] = load16(a.v_cache + off);
+        pk[k] = load16_stream(a.k_cache + off);
+        pv[k] = load16_stream(a.v_cache + off);
       } else {
         pk[k] = u32x4{0u, 0u, 0u, 0u};
         pv[k] = u32x4{0u, 0u, 0u, 0u};
