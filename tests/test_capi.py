@@ -56,7 +56,7 @@ def test_decode_plan_sizes():
     ((4, 64, 2, 256, 16, 100, 2048), _lib.TI_EUNSUPPORTED),   # group of 32 > 16-row tile
     ((4, 24, 4, 96, 16, 100, 2048), _lib.TI_EUNSUPPORTED),    # head_dim not built
     ((4, 24, 4, 256, 16, 100, 100), _lib.TI_EINVAL),          # split not a multiple of 32
-    ((4, 24, 4, 256, 16, 100, 16384), _lib.TI_EINVAL),        # split above the maximum
+    ((4, 24, 4, 256, 16, 100, 32768), _lib.TI_EINVAL),        # split above the maximum
     ((4, 25, 4, 256, 16, 100, 2048), _lib.TI_EINVAL),         # Hq not a multiple of Hkv
 ])
 def test_decode_plan_rejects(args, code):

@@ -7,8 +7,8 @@
 
 namespace ti {
 
-constexpr int kMaxSplitPages = 512;  // block ids of one partition staged in LDS
-constexpr int kMaxSplitTokens = 8192;
+constexpr int kMaxSplitPages = 1024;  // block ids of one partition staged in LDS
+constexpr int kMaxSplitTokens = 16384;
 
 struct Bf16 {};
 struct F16 {};

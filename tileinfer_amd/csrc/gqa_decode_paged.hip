@@ -14,29 +14,42 @@
 // reference kernel does at 50 and 138-142), fp32 accumulation, P rounded to the cache dtype before
 // the P.V product (as the reference kernel does at 148 and the torch recipe at 459-460).
 //
-// MFMA layout (v_mfma_f32_16x16x32_{bf16,f16}, lane l: row/col l%16, k-group l/16 of 8 values):
-//   S^T[16 tokens x 16 heads] = K[16 tokens x 32 d] . Q^T[32 d x 16 heads]   (D/32 steps)
-//     A = K rows straight from the page (lane (m,g): token m, d in [32kk+8g, +8)),
-//     B = the query group, rows >= group are zero; C leaves lane (n,g) holding tokens 4g..4g+3
-//     of head n.
-//   O^T[16 d x 16 heads] += V^T[16 d x 32 tokens] . P^T[32 tokens x 16 heads]  (D/16 tiles)
-//     B = P taken as-is from the S^T accumulators of two 16-token sub-tiles (no transpose),
-//     A = V rows gathered so that lane (m,g) owns d = 128c+8m+e (e < 8) of the same 8 tokens,
-//     assembled with v_perm_b32; C leaves lane (n,g) holding head n, d in [128c+32g, +32).
-// The head of every O^T accumulator is its lane's head, so the softmax rescale needs no
-// cross-lane traffic; only the running max crosses the 4 lanes that share a head.
+// Matrix-core layout, per 16-token tile (lane l: row/column l%16, k-group g = l/16):
+//   S^T[16 tokens x 16 heads] = K[16 tokens x 32 d] . Q^T[32 d x 16 heads]
+//     v_mfma_f32_16x16x32 x D/32: A = K rows straight from the page (lane (m,g): token m,
+//     d in [32kk+8g, +8)); B = the query group with rows >= group zero. The accumulator leaves
+//     lane (n,g) holding tokens 4g..4g+3 of head n.
+//   O^T[16 d x 16 heads] += V^T[16 d x 16 tokens] . P^T[16 tokens x 16 heads]
+//     v_mfma_f32_16x16x16 x D/16: B = P exactly as the S^T accumulator holds it (lane (n,g):
+//     tokens 4g..4g+3 of head n, no transpose); A = V gathered so that lane (m,g) owns
+//     d = 128c+8m+e (e < 8) of tokens 4g..4g+3, paired with v_perm_b32. The accumulator leaves
+//     lane (n,g) holding head n at d in [128c+32g, +32).
+// Every O^T accumulator's head is its lane's head, so the softmax rescale needs no cross-lane
+// traffic; only the running max crosses the 4 lanes that share a head.
 #include "decode_common.h"
 
 namespace ti {
 namespace {
 
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c, Bf16) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, a),
+                                                   __builtin_bit_cast(bf16x4_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c, F16) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a),
+                                               __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
+}
+
+// One 16-token tile of one KV head in MFMA operand layout.
 template <int D>
 struct Tile {
-  static constexpr int KK = D / 32;   // q.k MFMA steps
-  static constexpr int NC = D / 128;  // 16-byte d-chunks per lane per V row
-  u32x4 k[2][KK];                     // [sub-tile][k-step]
-  u32x4 v[2][4][NC];                  // [sub-tile][row 4g+r][chunk]
-  int rows[2];                        // tokens present in each sub-tile (uniform)
+  u32x4 k[D / 32];      // [k-step]: row n, d in [32kk+8g, +8)
+  u32x4 v[4][D / 128];  // [row 4g+r][chunk c]: d in [128c+8n, +8)
+  int rows;             // tokens of the tile that exist (uniform)
 };
 
 template <int D, typename Tag, int WPB>
@@ -83,7 +96,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
     }
   }
 
-  // Byte offsets of this lane's loads inside one 16-token sub-tile of its KV head.
+  // Byte offsets of this lane's loads inside one 16-token tile of its KV head.
   const uint32_t row_bytes = uint32_t(a.row_stride) * 2;
   const uint32_t lane_k = uint32_t(n) * row_bytes + 16 * g;
   const uint32_t lane_v = uint32_t(4 * g) * row_bytes + 16 * n;
@@ -94,107 +107,84 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
   float m_run = -INFINITY;
   float l_run = 0.f;
 
-  // Loads one 32-token tile (two 16-token sub-tiles) at position t0 into `T`. Every load is
-  // issued unconditionally through a buffer descriptor that spans only the sub-tile's rows that
-  // exist (in the partition and with a valid block id); rows past it read as zero with no memory
-  // access. Branch-free loads keep the compiler's count of outstanding loads exact, so waiting
-  // for one tile never waits for the tile prefetched behind it.
-  auto load_tile = [&](Tile<D>& T, int t0) {
+  // Loads the 16-token tile at position p into `T`. Every load is issued unconditionally through
+  // a buffer descriptor that spans only the tile's rows that exist (in the partition and with a
+  // valid block id); rows past it read as zero with no memory access. Branch-free loads keep the
+  // compiler's count of outstanding loads exact, so waiting for one tile never waits for the tile
+  // prefetched behind it.
+  auto load_tile = [&](Tile<D>& T, int p) {
+    // Past the partition end the LDS entry may be stale; `rows` is 0 there and masks it.
+    const int slot = min((p - tok0) / a.page_size, kMaxSplitPages - 1);
+    const int id = __builtin_amdgcn_readfirstlane(s_bids[slot]);
+    const bool ok = (tok1 - p > 0) && (uint32_t(id) < uint32_t(a.num_blocks32));
+    const int rows = ok ? min(tok1 - p, 16) : 0;
+    const int bid = ok ? id : 0;
+    const int64_t base =
+        int64_t(bid) * a.page_stride + int64_t(p % a.page_size) * a.row_stride + kvh * D;
+    const uint32_t nbytes = rows > 0 ? uint32_t(rows - 1) * row_bytes + D * 2 : 0u;
+    const auto rk = make_rsrc(a.k_cache + base, nbytes);
+    const auto rv = make_rsrc(a.v_cache + base, nbytes);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int p = t0 + 16 * i;
-      // Past the partition end the LDS entry may be stale; `rows` is 0 there and masks it.
-      const int slot = min((p - tok0) / a.page_size, kMaxSplitPages - 1);
-      const int id = __builtin_amdgcn_readfirstlane(s_bids[slot]);
-      const bool ok = (tok1 - p > 0) && (uint32_t(id) < uint32_t(a.num_blocks32));
-      const int rows = ok ? min(tok1 - p, 16) : 0;
-      const int bid = ok ? id : 0;
-      const int64_t base =
-          int64_t(bid) * a.page_stride + int64_t(p % a.page_size) * a.row_stride + kvh * D;
-      const uint32_t nbytes = rows > 0 ? uint32_t(rows - 1) * row_bytes + D * 2 : 0u;
-      const auto rk = make_rsrc(a.k_cache + base, nbytes);
-      const auto rv = make_rsrc(a.v_cache + base, nbytes);
+    for (int kk = 0; kk < KK; ++kk) T.k[kk] = buffer_load16(rk, lane_k + 64 * kk);
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) T.k[i][kk] = buffer_load16(rk, lane_k + 64 * kk);
+    for (int r = 0; r < 4; ++r) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) T.v[i][r][c] = buffer_load16(rv, lane_v + r * row_bytes + 256 * c);
-      }
-      T.rows[i] = rows;
+      for (int c = 0; c < NC; ++c) T.v[r][c] = buffer_load16(rv, lane_v + r * row_bytes + 256 * c);
     }
+    T.rows = rows;
   };
 
   auto compute_tile = [&](Tile<D>& T) {
-    f32x4 s[2];
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      s[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kk = 0; kk < KK; ++kk) s = mfma16x16x32(T.k[kk], qop[kk], s, Tag{});
+    float sv[4];
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) s[i] = mfma16x16x32(T.k[i][kk], qop[kk], s[i], Tag{});
-    }
-    float sv[8];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sv[4 * i + r] = (4 * g + r < T.rows[i]) ? s[i][r] * a.scale_log2 : -INFINITY;
-      }
-    }
-    float mx = sv[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
+    for (int r = 0; r < 4; ++r) sv[r] = (4 * g + r < T.rows) ? s[r] * a.scale_log2 : -INFINITY;
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
     const float alpha = fast_exp2(m_run - m_use);
-    float p[8];
-    float psum = 0.f;
+    float p[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      p[j] = fast_exp2(sv[j] - m_use);
-      psum += p[j];
-    }
-    l_run = l_run * alpha + psum;
+    for (int r = 0; r < 4; ++r) p[r] = fast_exp2(sv[r] - m_use);
+    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
     m_run = m_new;
     if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) o[t] *= alpha;
     }
-    // P^T operand: element j <-> token (sub-tile j/4, row 4g + j%4).
-    u32x4 pop;
+    // P^T operand: element j <-> token 4g + j.
+    u32x2 pop;
     pop[0] = pack2(p[0], p[1], Tag{});
     pop[1] = pack2(p[2], p[3], Tag{});
-    pop[2] = pack2(p[4], p[5], Tag{});
-    pop[3] = pack2(p[6], p[7], Tag{});
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
+        // V^T operand of d-tile 8c+e: (V[4g][d], V[4g+1][d]), (V[4g+2][d], V[4g+3][d]).
         const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        u32x4 vop;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int i = k >> 1;
-          const int r = 2 * (k & 1);
-          vop[k] = __builtin_amdgcn_perm(T.v[i][r + 1][c][e >> 1], T.v[i][r][c][e >> 1], sel);
-        }
-        o[8 * c + e] = mfma16x16x32(vop, pop, o[8 * c + e], Tag{});
+        u32x2 vop;
+        vop[0] = __builtin_amdgcn_perm(T.v[1][c][e >> 1], T.v[0][c][e >> 1], sel);
+        vop[1] = __builtin_amdgcn_perm(T.v[3][c][e >> 1], T.v[2][c][e >> 1], sel);
+        o[8 * c + e] = mfma16x16x16(vop, pop, o[8 * c + e], Tag{});
       }
     }
   };
 
-  const int ntiles = (tok1 - tok0 + 31) / 32;
+  // Two tiles in flight: the next tile's loads are issued before the current one is consumed.
+  const int ntiles = (tok1 - tok0 + 15) / 16;
   if (ntiles > 0) {
     Tile<D> ta, tb;
     load_tile(ta, tok0);
     int it = 0;
     for (; it + 2 <= ntiles; it += 2) {
-      const int t0 = tok0 + 32 * it;
-      load_tile(tb, t0 + 32);
+      const int t0 = tok0 + 16 * it;
+      load_tile(tb, t0 + 16);
       compute_tile(ta);
-      if (it + 2 < ntiles) load_tile(ta, t0 + 64);
+      if (it + 2 < ntiles) load_tile(ta, t0 + 32);
       compute_tile(tb);
     }
     if (it < ntiles) compute_tile(ta);
@@ -344,10 +334,14 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
                   split_req, (long long)unit, kMaxSplitTokens, kMaxSplitPages);
     }
   } else {
-    // Aim for >= 8 waves per CU over the whole grid without cutting partitions below 256 tokens.
-    const int64_t target_waves = int64_t(8) * device_cu_count();
-    split = 2048;
-    while (split > 256 && int64_t(batch) * hkv * ceil_div(bound, split) < target_waves) split /= 2;
+    // Fewest, longest partitions that still give every CU a workgroup: each workgroup pays a
+    // start-up (block ids, first tile) and drain that nothing else on its CU hides, so on MI355X
+    // one full round of long workgroups streams fastest (config 3: 8,192 tokens, 256 workgroups).
+    const int64_t cus = device_cu_count();
+    const int64_t wpb = (hkv % 4 == 0) ? 4 : (hkv % 2 == 0) ? 2 : 1;  // waves per workgroup
+    const int64_t wgs_per_split = int64_t(batch) * (hkv / wpb);
+    split = kMaxSplitTokens;
+    while (split > 256 && wgs_per_split * ceil_div(bound, split) < cus) split /= 2;
     split = ceil_div(split, unit) * unit;
     while (split / page_size > kMaxSplitPages) split -= unit;
     if (split <= 0) split = unit;
