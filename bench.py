@@ -175,10 +175,97 @@ def calibrate(dev, gib: float = 4.0, reps: int = 5):
           flush=True)
 
 
+def _time(fn, steps: int, warmup: int) -> float:
+    """Mean µs of fn() over `steps` calls after `warmup`, HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / steps
+
+
+def run_config(cfg: int, args, dev) -> dict:
+    """One attention layer of BASELINE config 1, 2, 4 or 5 (append, then decode), on the GPU."""
+    from tileinfer_amd import workloads as wl
+
+    extra = {}
+    if cfg == 1:
+        st = wl.config1(device=dev)
+    elif cfg == 2:
+        st = wl.config2(device=dev)
+    elif cfg == 4:
+        st, chunk_slots = wl.config4(device=dev)
+    elif cfg == 5:
+        st = wl.config5(device=dev)
+    else:
+        raise SystemExit(f"--config {cfg}: choose 1, 2, 3 (default), 4 or 5")
+    kc, vc = st.k_cache, st.v_cache
+    rows = lambda c: c.view(-1, HKV * HEAD_DIM)  # noqa: E731
+    if cfg == 4:
+        key = torch.cat([st.meta["chunk_k"], st.k_new])
+        val = torch.cat([st.meta["chunk_v"], st.v_new])
+        slots = torch.cat([chunk_slots, st.slot_mapping])
+    else:
+        key, val, slots = st.k_new, st.v_new, st.slot_mapping
+    ctx = st.seqlen.tolist()
+    a_us = _time(lambda: store_kvcache(key, val, rows(kc), rows(vc), slots), args.steps, args.warmup)
+    reuse = cfg == 5  # tables alias one prefix: keep K/V cacheable (PagedKVManager.shares_blocks)
+    d_us = _time(lambda: gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen,
+                                             split_tokens=args.split_tokens,
+                                             variant=args.variant, kv_reuse=reuse),
+                 args.steps, args.warmup)
+    a_bytes = append_bytes(slots, HKV * HEAD_DIM)
+    d_bytes = decode_bytes(ctx)
+    if cfg == 4:
+        # Also as two calls (chunk, then the 32 decode tokens), and a bulk append rate.
+        two = _time(lambda: (store_kvcache(st.meta["chunk_k"], st.meta["chunk_v"], rows(kc),
+                                           rows(vc), chunk_slots),
+                             store_kvcache(st.k_new, st.v_new, rows(kc), rows(vc),
+                                           st.slot_mapping)), args.steps, args.warmup)
+        n = 65536
+        gen = torch.Generator(device=dev).manual_seed(5)
+        bk = torch.randn((n, HKV, HEAD_DIM), generator=gen, device=dev).to(torch.bfloat16)
+        bv = torch.randn((n, HKV, HEAD_DIM), generator=gen, device=dev).to(torch.bfloat16)
+        bs = torch.randperm(kc.shape[0] * BLOCK, generator=gen, device=dev)[:n].to(torch.int32)
+        b_us = _time(lambda: store_kvcache(bk, bv, rows(kc), rows(vc), bs), args.steps, args.warmup)
+        extra = {"append_two_calls_us": round(two, 2),
+                 "append_bulk_65536_us": round(b_us, 2),
+                 "append_bulk_GBps_algorithmic": round(append_bytes(bs, HKV * HEAD_DIM) / (b_us * 1e-6) / 1e9, 1)}
+    if cfg == 5:
+        unique = int(torch.unique(st.block_table).numel())
+        stream_us = _time(lambda: gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen,
+                                                      split_tokens=args.split_tokens,
+                                                      variant=args.variant), args.steps, args.warmup)
+        extra = {"decode_us_streaming_policy": round(stream_us, 2),
+                 "decode_logical_bytes": d_bytes,
+                 "decode_physical_unique_kv_bytes": unique * 2 * BLOCK * HKV * HEAD_DIM * 2,
+                 "note": "shared prefix blocks are re-read from L2/MALL, so the logical rate can "
+                         "exceed HBM peak; rocprof FETCH_SIZE gives the HBM share"}
+    split, max_splits, _ = decode_plan(len(ctx), HQ, HKV, HEAD_DIM, BLOCK,
+                                       st.block_table.shape[1], args.split_tokens)
+    return {
+        "metric": METRIC, "config": {"workload": f"config{cfg}", "batch": len(ctx),
+                                     "ctx_min": min(ctx), "ctx_max": max(ctx), "ctx_sum": sum(ctx),
+                                     "append_tokens": slots.numel(), "split_tokens": split,
+                                     "max_splits": max_splits, "variant": args.variant},
+        "decode_us": round(d_us, 2), "decode_GBps_algorithmic": round(d_bytes / (d_us * 1e-6) / 1e9, 1),
+        "decode_pct_of_peak_hbm": round(100 * d_bytes / (d_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 2),
+        "append_us": round(a_us, 2), "append_GBps_algorithmic": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
+        "us_per_layer_step": round(a_us + d_us, 2), **extra,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--calibrate", action="store_true",
                     help="run only the copy/read calibration of known size and exit")
+    ap.add_argument("--config", type=int, default=3,
+                    help="BASELINE config: 3 (default, the headline line) or 1, 2, 4, 5 (one layer)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
@@ -205,6 +292,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.calibrate:
         calibrate(dev)
+        return
+    if args.config != 3:
+        print(json.dumps(run_config(args.config, args, dev)), flush=True)
         return
     b, ctx, layers = args.batch, args.ctx, args.layers
     log(f"allocating cache: batch {b} x ctx {ctx} x {layers} layers")

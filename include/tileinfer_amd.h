@@ -37,6 +37,10 @@ extern "C" {
 #define TI_DECODE_AUTO 0   /* the measured-fastest variant for the shape */
 #define TI_DECODE_MFMA 1   /* query group packed into a 16-row MFMA tile, K/V direct to registers */
 #define TI_DECODE_SCALAR 2 /* K/V pages staged in LDS, fp32 FMA, DPP/shuffle softmax reductions */
+/* Flag OR'd into `variant`: the call's block tables share pages across sequences (prefix caching),
+ * so K/V is loaded with the default cache policy and shared pages are served from L2/MALL. Without
+ * it K/V is loaded as a once-read stream (`nt`), faster when every page is read once per call. */
+#define TI_DECODE_REUSE_KV 0x10
 
 /*
  * Slot-mapped K/V append: for every i in [0, n_tokens) with 0 <= slot_mapping[i] < num_slots,
@@ -93,7 +97,8 @@ int ti_gqa_decode_plan(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
  *   out          [batch, num_q_heads, head_dim] contiguous
  *   workspace    >= workspace_bytes from ti_gqa_decode_plan with the same arguments (may be NULL
  *                when that is 0); contents need no initialisation.
- *   split_tokens as in ti_gqa_decode_plan; variant one of TI_DECODE_*.
+ *   split_tokens as in ti_gqa_decode_plan; variant one of TI_DECODE_AUTO/MFMA/SCALAR, optionally
+ *                OR'd with TI_DECODE_REUSE_KV.
  */
 int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
                         const void* v_cache, const int32_t* block_table, int64_t block_table_stride,

@@ -31,9 +31,10 @@ def test_library_exports_every_declared_symbol():
 def test_header_codes_match_binding():
     text = HEADER.read_text()
     for name in ("TI_OK", "TI_EINVAL", "TI_ELAUNCH", "TI_EUNSUPPORTED", "TI_DTYPE_BF16",
-                 "TI_DTYPE_F16", "TI_DECODE_AUTO", "TI_DECODE_MFMA", "TI_DECODE_SCALAR"):
-        m = re.search(rf"#define {name} (\d+)", text)
-        assert m and int(m.group(1)) == getattr(_lib, name), name
+                 "TI_DTYPE_F16", "TI_DECODE_AUTO", "TI_DECODE_MFMA", "TI_DECODE_SCALAR",
+                 "TI_DECODE_REUSE_KV"):
+        m = re.search(rf"#define {name} (0x[0-9a-fA-F]+|\d+)", text)
+        assert m and int(m.group(1), 0) == getattr(_lib, name), name
 
 
 def _plan(*args):

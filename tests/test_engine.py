@@ -165,6 +165,19 @@ def test_manager_prefix_hit_shares_and_allocates_rest():
     assert m.block_manager.num_free_blocks == 20
 
 
+def test_manager_shares_blocks_hint():
+    m = PagedKVManager(20, 16)
+    a = Sequence(list(range(40)))
+    m.admit(a)
+    assert not m.shares_blocks([a])
+    m.finish_chunk(a, 32)
+    b = Sequence(list(range(32)) + [7] * 9)
+    m.admit(b)
+    c = Sequence([5] * 20)
+    m.admit(c)
+    assert m.shares_blocks([a, b]) and m.shares_blocks([b]) and not m.shares_blocks([c])
+
+
 def test_manager_full_prefix_match_leaves_a_token_to_prefill():
     m = PagedKVManager(10, 16)
     a = Sequence(list(range(32)))

@@ -102,12 +102,18 @@ def test_shared_vs_private_prefix_bitwise(dev):
     say("decode shared vs private (config5 at batch 8)")
     shared = config5(batch=8, device=dev, shared=True)
     private = config5(batch=8, device=dev, shared=False)
+    o1 = None
     for variant in VARIANTS:
-        o1 = gqa_decode_paged_fn(shared.q, shared.k_cache, shared.v_cache, shared.block_table,
-                                 shared.seqlen, variant=variant)
-        o2 = gqa_decode_paged_fn(private.q, private.k_cache, private.v_cache, private.block_table,
-                                 private.seqlen, variant=variant)
-        assert torch.equal(bits(o1), bits(o2)), variant
+        for reuse in (False, True):
+            a = gqa_decode_paged_fn(shared.q, shared.k_cache, shared.v_cache, shared.block_table,
+                                    shared.seqlen, variant=variant, kv_reuse=reuse)
+            b = gqa_decode_paged_fn(private.q, private.k_cache, private.v_cache,
+                                    private.block_table, private.seqlen, variant=variant,
+                                    kv_reuse=reuse)
+            assert torch.equal(bits(a), bits(b)), (variant, reuse)
+            if variant == "mfma":
+                o1 = a if o1 is None else o1
+                assert torch.equal(bits(a), bits(o1)), "the cache policy changed the result"
     # And against the oracle for two sampled sequences (CPU copies of their blocks only).
     for i in (0, 5):
         pages = shared.block_table[i].long()

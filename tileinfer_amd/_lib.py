@@ -24,6 +24,7 @@ TI_DTYPE_F16 = 1
 TI_DECODE_AUTO = 0
 TI_DECODE_MFMA = 1
 TI_DECODE_SCALAR = 2
+TI_DECODE_REUSE_KV = 0x10
 ABI_VERSION = 1
 
 # Every symbol declared in include/tileinfer_amd.h, with its ctypes signature.

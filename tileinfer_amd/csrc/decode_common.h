@@ -52,18 +52,27 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t* base
                                            kBufferRsrcWord3);
 }
 
-// Cache policy of a load that streams data read exactly once (K/V pages): the `nt` bit. On
-// MI355X a read stream issued this way sustains ~7.1 TB/s against ~6.3 TB/s with the default
-// policy.
+// Cache policies of the K/V loads. kPolicyStream (the `nt` bit) is for pages read once per call:
+// on MI355X a read stream issued that way sustains ~7.0 TB/s against ~6.3 TB/s with the default
+// policy. kPolicyKeep (default policy) is for calls whose block tables share pages across
+// sequences (prefix caching): the shared pages are then served from L2/MALL, which `nt` defeats
+// (config 5: 450 us with kPolicyKeep against 770 us with kPolicyStream).
+constexpr int kPolicyKeep = 0;
 constexpr int kPolicyStream = 2;
 
+template <int POL>
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset) {
-  return __builtin_bit_cast(
-      u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, int(offset), 0, kPolicyStream));
+  return __builtin_bit_cast(u32x4,
+                            __builtin_amdgcn_raw_buffer_load_b128(rsrc, int(offset), 0, POL));
 }
 
-__device__ __forceinline__ u32x4 load16_stream(const uint16_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+template <int POL>
+__device__ __forceinline__ u32x4 load16_policy(const uint16_t* p) {
+  if constexpr (POL == kPolicyStream) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  } else {
+    return load16(p);
+  }
 }
 
 struct DecodeArgs {
@@ -94,7 +103,7 @@ __device__ __forceinline__ int seq_len(const DecodeArgs& a, int b) {
 
 
 // Launches the LDS-staged scalar variant of the partial kernel (gqa_decode_scalar.hip).
-int launch_decode_scalar(const DecodeArgs& a, int batch, bool bf16, int head_dim,
+int launch_decode_scalar(const DecodeArgs& a, int batch, bool bf16, int head_dim, bool reuse_kv,
                          hipStream_t stream);
 
 }  // namespace ti

@@ -52,7 +52,7 @@ struct Tile {
   int rows;             // tokens of the tile that exist (uniform)
 };
 
-template <int D, typename Tag, int WPB>
+template <int D, typename Tag, int WPB, int POL>
 __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
   constexpr int KK = D / 32;
   constexpr int NC = D / 128;
@@ -125,11 +125,11 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
     const auto rk = make_rsrc(a.k_cache + base, nbytes);
     const auto rv = make_rsrc(a.v_cache + base, nbytes);
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) T.k[kk] = buffer_load16(rk, lane_k + 64 * kk);
+    for (int kk = 0; kk < KK; ++kk) T.k[kk] = buffer_load16<POL>(rk, lane_k + 64 * kk);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c) T.v[r][c] = buffer_load16(rv, lane_v + r * row_bytes + 256 * c);
+      for (int c = 0; c < NC; ++c) T.v[r][c] = buffer_load16<POL>(rv, lane_v + r * row_bytes + 256 * c);
     }
     T.rows = rows;
   };
@@ -269,22 +269,27 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
 }
 
 template <int D, typename Tag, int WPB>
-int launch_mfma(const DecodeArgs& a, int batch, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB>), dim3(a.hkv / WPB, a.max_splits, batch),
-                     dim3(64 * WPB), 0, stream, a);
+int launch_mfma(const DecodeArgs& a, int batch, bool reuse_kv, hipStream_t stream) {
+  const dim3 grid(a.hkv / WPB, a.max_splits, batch);
+  if (reuse_kv) {
+    hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyKeep>), grid, dim3(64 * WPB), 0,
+                       stream, a);
+  } else {
+    hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyStream>), grid, dim3(64 * WPB), 0,
+                       stream, a);
+  }
   return check_launch("ti_gqa_decode_paged (mfma)");
 }
 
 template <int D, typename Tag>
-int launch_decode(const DecodeArgs& a, int batch, int variant, hipStream_t stream) {
-  (void)variant;  // the scalar variant is dispatched by launch_decode_scalar
+int launch_decode(const DecodeArgs& a, int batch, bool reuse_kv, hipStream_t stream) {
   int rc;
   if (a.hkv % 4 == 0) {
-    rc = launch_mfma<D, Tag, 4>(a, batch, stream);
+    rc = launch_mfma<D, Tag, 4>(a, batch, reuse_kv, stream);
   } else if (a.hkv % 2 == 0) {
-    rc = launch_mfma<D, Tag, 2>(a, batch, stream);
+    rc = launch_mfma<D, Tag, 2>(a, batch, reuse_kv, stream);
   } else {
-    rc = launch_mfma<D, Tag, 1>(a, batch, stream);
+    rc = launch_mfma<D, Tag, 1>(a, batch, reuse_kv, stream);
   }
   if (rc != TI_OK) return rc;
   if (a.max_splits > 1) {
@@ -381,8 +386,11 @@ extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_
   if (dtype != TI_DTYPE_BF16 && dtype != TI_DTYPE_F16) {
     return fail(TI_EUNSUPPORTED, "ti_gqa_decode_paged: dtype code %d is not bf16/fp16", dtype);
   }
-  if (variant != TI_DECODE_AUTO && variant != TI_DECODE_MFMA && variant != TI_DECODE_SCALAR) {
-    return fail(TI_EINVAL, "ti_gqa_decode_paged: unknown variant %d", variant);
+  const int kind = variant & 0xF;
+  const bool reuse_kv = (variant & TI_DECODE_REUSE_KV) != 0;
+  if ((kind != TI_DECODE_AUTO && kind != TI_DECODE_MFMA && kind != TI_DECODE_SCALAR) ||
+      (variant & ~(0xF | TI_DECODE_REUSE_KV)) != 0) {
+    return fail(TI_EINVAL, "ti_gqa_decode_paged: unknown variant/flags 0x%x", variant);
   }
   int32_t split = 0, max_splits = 0;
   int64_t ws_need = 0;
@@ -432,8 +440,8 @@ extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_
   a.scale_log2 = float(1.4426950408889634 / sqrt(double(head_dim)));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf16 = dtype == TI_DTYPE_BF16;
-  if (variant == TI_DECODE_SCALAR) {
-    rc = launch_decode_scalar(a, batch, bf16, head_dim, s);
+  if (kind == TI_DECODE_SCALAR) {
+    rc = launch_decode_scalar(a, batch, bf16, head_dim, reuse_kv, s);
     if (rc != TI_OK) return rc;
     if (max_splits > 1) {
       if (head_dim == 256) {
@@ -448,9 +456,9 @@ extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_
     return TI_OK;
   }
   if (head_dim == 256) {
-    return bf16 ? launch_decode<256, Bf16>(a, batch, variant, s)
-                : launch_decode<256, F16>(a, batch, variant, s);
+    return bf16 ? launch_decode<256, Bf16>(a, batch, reuse_kv, s)
+                : launch_decode<256, F16>(a, batch, reuse_kv, s);
   }
-  return bf16 ? launch_decode<128, Bf16>(a, batch, variant, s)
-              : launch_decode<128, F16>(a, batch, variant, s);
+  return bf16 ? launch_decode<128, Bf16>(a, batch, reuse_kv, s)
+              : launch_decode<128, F16>(a, batch, reuse_kv, s);
 }

@@ -39,7 +39,7 @@ __device__ __forceinline__ uint16_t from_float(float v, F16) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
 }
 
-template <int D, int G, typename Tag>
+template <int D, int G, typename Tag, int POL>
 __global__ __launch_bounds__(256) void decode_scalar_kernel(DecodeArgs a) {
   constexpr int TT = 64;                // tokens per staged tile
   constexpr int ROW = D + 8;            // padded LDS row (16-bit elements)
@@ -99,8 +99,8 @@ __global__ __launch_bounds__(256) void decode_scalar_kernel(DecodeArgs a) {
       if (bid >= 0) {
         const int64_t off = int64_t(bid) * a.page_stride + int64_t(pos % a.page_size) * a.row_stride +
                             int64_t(kvh) * D + 8 * col;
-        pk[k] = load16_stream(a.k_cache + off);
-        pv[k] = load16_stream(a.v_cache + off);
+        pk[k] = load16_policy<POL>(a.k_cache + off);
+        pv[k] = load16_policy<POL>(a.v_cache + off);
       } else {
         pk[k] = u32x4{0u, 0u, 0u, 0u};
         pv[k] = u32x4{0u, 0u, 0u, 0u};
@@ -258,18 +258,28 @@ __global__ __launch_bounds__(256) void decode_scalar_kernel(DecodeArgs a) {
   }
 }
 
+template <int D, int G, typename Tag>
+void launch_gp(const DecodeArgs& a, dim3 grid, bool reuse_kv, hipStream_t stream) {
+  if (reuse_kv) {
+    hipLaunchKernelGGL((decode_scalar_kernel<D, G, Tag, kPolicyKeep>), grid, dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((decode_scalar_kernel<D, G, Tag, kPolicyStream>), grid, dim3(256), 0, stream,
+                       a);
+  }
+}
+
 template <int D, typename Tag>
-int launch_g(const DecodeArgs& a, int batch, hipStream_t stream) {
+int launch_g(const DecodeArgs& a, int batch, bool reuse_kv, hipStream_t stream) {
   const dim3 grid(a.hkv, a.max_splits, batch);
   switch (a.group) {
     case 4:
-      hipLaunchKernelGGL((decode_scalar_kernel<D, 4, Tag>), grid, dim3(256), 0, stream, a);
+      launch_gp<D, 4, Tag>(a, grid, reuse_kv, stream);
       break;
     case 6:
-      hipLaunchKernelGGL((decode_scalar_kernel<D, 6, Tag>), grid, dim3(256), 0, stream, a);
+      launch_gp<D, 6, Tag>(a, grid, reuse_kv, stream);
       break;
     case 8:
-      hipLaunchKernelGGL((decode_scalar_kernel<D, 8, Tag>), grid, dim3(256), 0, stream, a);
+      launch_gp<D, 8, Tag>(a, grid, reuse_kv, stream);
       break;
     default:
       return fail(TI_EUNSUPPORTED, "scalar decode: query group %d not built (4, 6, 8)", a.group);
@@ -279,10 +289,16 @@ int launch_g(const DecodeArgs& a, int batch, hipStream_t stream) {
 
 }  // namespace
 
-int launch_decode_scalar(const DecodeArgs& a, int batch, bool bf16, int head_dim,
+int launch_decode_scalar(const DecodeArgs& a, int batch, bool bf16, int head_dim, bool reuse_kv,
                          hipStream_t stream) {
-  if (head_dim == 256) return bf16 ? launch_g<256, Bf16>(a, batch, stream) : launch_g<256, F16>(a, batch, stream);
-  if (head_dim == 128) return bf16 ? launch_g<128, Bf16>(a, batch, stream) : launch_g<128, F16>(a, batch, stream);
+  if (head_dim == 256) {
+    return bf16 ? launch_g<256, Bf16>(a, batch, reuse_kv, stream)
+                : launch_g<256, F16>(a, batch, reuse_kv, stream);
+  }
+  if (head_dim == 128) {
+    return bf16 ? launch_g<128, Bf16>(a, batch, reuse_kv, stream)
+                : launch_g<128, F16>(a, batch, reuse_kv, stream);
+  }
   return fail(TI_EUNSUPPORTED, "scalar decode: head_dim %d not built", head_dim);
 }
 

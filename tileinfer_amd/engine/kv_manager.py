@@ -83,3 +83,9 @@ class PagedKVManager:
 
     def free(self, seq: Sequence) -> list[int]:
         return self.block_manager.deallocate(seq)
+
+    def shares_blocks(self, seqs: list[Sequence]) -> bool:
+        """Whether any block of these sequences is held by more than one sequence: the decode
+        hint ``kv_reuse`` (shared pages are then worth keeping in cache)."""
+        blocks = self.block_manager.blocks
+        return any(blocks[b].ref_count > 1 for s in seqs for b in s.block_table)

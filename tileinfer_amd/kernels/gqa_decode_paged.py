@@ -58,6 +58,7 @@ def gqa_decode_paged_fn(
     out: torch.Tensor | None = None,
     split_tokens: int | None = None,
     variant: str = "auto",
+    kv_reuse: bool = False,
 ) -> torch.Tensor:
     """Single-query paged GQA attention.
 
@@ -70,6 +71,10 @@ def gqa_decode_paged_fn(
         out: keyword-only preallocated [B, H_q, D] output (contiguous, q's dtype)
         split_tokens: keyword-only split-K partition length (None: the library's choice)
         variant: keyword-only "auto" | "mfma" | "scalar" kernel choice
+        kv_reuse: keyword-only; True when the block tables share pages across sequences (prefix
+            caching), so K/V keeps the default cache policy and shared pages hit in L2/MALL; the
+            default streams every page once (``nt``), which is faster when nothing is shared.
+            Results are bitwise identical either way.
     Returns:
         [B, H_q, D] tensor in q's dtype.
     """
@@ -132,5 +137,6 @@ def gqa_decode_paged_fn(
         block_table.data_ptr(), block_table.stride(0) if width > 0 else 0, seqlen_kv.data_ptr(),
         out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes,
         b, h_q, h_kv, d, page_size, rows // page_size, width, int(split_tokens or 0),
-        _VARIANTS[variant], code, _lib.stream_handle(dev)))
+        _VARIANTS[variant] | (_lib.TI_DECODE_REUSE_KV if kv_reuse else 0), code,
+        _lib.stream_handle(dev)))
     return out
