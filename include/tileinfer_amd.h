@@ -107,6 +107,26 @@ int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h, c
                         int32_t page_size, int64_t num_blocks, int32_t max_blocks_per_seq,
                         int32_t split_tokens, int32_t variant, int32_t dtype, void* stream);
 
+/*
+ * Whole-block copy between two paged caches (device or pinned host memory, in any direction):
+ * for every pair i, block block_pairs[2i] of `src` is copied to block block_pairs[2i+1] of `dst`.
+ * A block consists of `n_chunks` chunks of `chunk_bytes`; chunk c of block b starts at
+ * base + c * chunk_stride_bytes + b * chunk_bytes (for the [2, layers, blocks, ...] cache slab:
+ * n_chunks = 2 * layers, chunk_bytes = one layer's K or V block, chunk_stride = blocks *
+ * chunk_bytes). `src`/`dst` must span n_chunks * their chunk stride; `block_pairs` is int64
+ * [n_pairs, 2] in device-readable memory. Pairs with an id outside [0, num_blocks) are skipped.
+ * Destination blocks must be distinct. One launch on `stream`; pinned host memory is accessed
+ * directly by the kernel.
+ *
+ * No reference counterpart: tileInfer accepts a swap budget but never moves KV blocks
+ * (engine/config.py:22, engine/block_manager.py:29); this is the data path of block swapping and
+ * copy-on-write.
+ */
+int ti_copy_blocks(const void* src, void* dst, const int64_t* block_pairs, int64_t n_pairs,
+                   int32_t n_chunks, int64_t chunk_bytes, int64_t src_chunk_stride_bytes,
+                   int64_t dst_chunk_stride_bytes, int64_t src_num_blocks, int64_t dst_num_blocks,
+                   void* stream);
+
 /* Text of the last error reported on the calling thread ("" when none). */
 const char* ti_last_error(void);
 

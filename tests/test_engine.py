@@ -288,3 +288,39 @@ def test_attention_context_is_thread_local():
     assert seen == [None] and get_context() is ctx
     reset_context()
     assert get_context() is None
+
+
+# ----------------------------------------------------------------------------- swapping
+
+
+def test_swap_out_moves_only_unshared_blocks():
+    m = PagedKVManager(12, 16, num_host_blocks=4)
+    a = Sequence(list(range(40)))
+    m.admit(a)                                   # blocks 0, 1, 2
+    m.finish_chunk(a, 32)
+    b = Sequence(list(range(32)) + [9] * 30)
+    m.admit(b)                                   # shares 0, 1; owns 3, 4
+    assert b.block_table == [0, 1, 3, 4]
+    pairs = m.swap_out(b)
+    assert pairs == [(3, 0), (4, 1)]             # host slots handed out 0, 1 (LIFO pool)
+    assert b.block_table == [0, 1, -1, -1]
+    assert m.block_manager.blocks[3].ref_count == 0 and 3 in m.block_manager.free_block_ids
+    assert m.block_manager.blocks[0].ref_count == 2
+    assert m.can_swap_in(b)
+    back = m.swap_in(b)
+    assert [slot for slot, _ in back] == [0, 1]
+    assert b.block_table[:2] == [0, 1] and -1 not in b.block_table
+    assert sorted(m.host_free) == [0, 1, 2, 3]
+    assert [bid for _, bid in back] == b.block_table[2:]
+
+
+def test_swap_pool_exhaustion_and_free_while_swapped():
+    m = PagedKVManager(10, 16, num_host_blocks=1)
+    a = Sequence(list(range(40)))
+    m.admit(a)
+    with pytest.raises(RuntimeError):
+        m.swap_out(a)                            # 3 unshared blocks, 1 host slot
+    assert a.block_table == [0, 1, 2]            # nothing changed
+    assert m.swap_out(a, max_blocks=1) == [(0, 0)]
+    m.free(a)                                    # freeing a swapped sequence returns its host slot
+    assert m.host_free == [0] and m.block_manager.num_free_blocks == 10

@@ -109,6 +109,23 @@ class BlockManager:
         seq.block_table.clear()
         return freed
 
+    def allocate_block(self) -> int:
+        """Take one free block (reference count 1); the caller places it in a table."""
+        return self._allocate_block()
+
+    def release(self, block_id: int) -> bool:
+        """Drop one reference to ``block_id``; returns True when that freed it."""
+        block = self.blocks[block_id]
+        if block.ref_count <= 0:
+            raise ValueError(f"block {block_id} is already free")
+        block.ref_count -= 1
+        if block.ref_count == 0:
+            self._deallocate_block(block_id)
+            if self.on_block_freed is not None:
+                self.on_block_freed(block_id)
+            return True
+        return False
+
     def _blocks_needed_for_append(self, seq: Sequence) -> int:
         short = max(0, seq.num_blocks - len(seq.block_table))   # slots missing for len(seq) tokens
         ahead = 1 if len(seq) % self.block_size == 0 else 0     # the reference's early trigger

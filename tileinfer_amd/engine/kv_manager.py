@@ -16,6 +16,12 @@ holds, without its batching policy:
 One fix: the reference can match every block of a prompt whose length is a multiple of the block
 size, leaving nothing to prefill, so the sequence is never scheduled (engine/scheduler.py:127-131).
 Here a match is cut back by one block when it would cover the whole prompt.
+
+Swapping (advertised by the reference, never implemented: engine/config.py:22,
+engine/block_manager.py:29): ``swap_out`` moves a sequence's unshared blocks to slots of a pinned
+host pool and frees them on the device; ``swap_in`` brings them back into fresh device blocks at
+the same logical positions. Both return the ``(source, destination)`` pairs that
+``tileinfer_amd.kernels.block_copy.swap_blocks`` executes; shared (prefix) blocks stay resident.
 """
 from __future__ import annotations
 
@@ -27,9 +33,12 @@ from .sequence import Sequence
 
 
 class PagedKVManager:
-    def __init__(self, num_blocks: int, block_size: int, enable_prefix_caching: bool = True):
+    def __init__(self, num_blocks: int, block_size: int, enable_prefix_caching: bool = True,
+                 num_host_blocks: int = 0):
         self.block_size = block_size
         self.block_manager = BlockManager(num_blocks, block_size)
+        self.host_free: list[int] = list(range(num_host_blocks - 1, -1, -1))
+        self.swapped: dict[int, list[tuple[int, int]]] = {}  # seq_id -> [(table index, host slot)]
         self.prefix_cache = PrefixCache(block_size)
         self.enable_prefix_caching = enable_prefix_caching
         self.on_block_freed: Callable[[int], None] | None = None
@@ -82,10 +91,59 @@ class PagedKVManager:
             self.prefix_cache.add(seq.token_ids[:seq.num_cached_tokens], seq.block_table)
 
     def free(self, seq: Sequence) -> list[int]:
+        for _, slot in self.swapped.pop(seq.seq_id, []):
+            self.host_free.append(slot)
+        seq.block_table[:] = [b for b in seq.block_table if b >= 0]
         return self.block_manager.deallocate(seq)
+
+    def swap_out(self, seq: Sequence, max_blocks: int | None = None) -> list[tuple[int, int]]:
+        """Move up to ``max_blocks`` of the sequence's unshared blocks to host slots.
+
+        Returns ``(device block, host slot)`` pairs to copy device -> host before the freed device
+        blocks are reused (stream order does that when both run on one stream). The table keeps
+        -1 at swapped positions until ``swap_in``. Raises if the host pool is too small.
+        """
+        if seq.seq_id in self.swapped:
+            raise ValueError(f"sequence {seq.seq_id} is already swapped out")
+        bm = self.block_manager
+        todo = [i for i, b in enumerate(seq.block_table) if b >= 0 and bm.blocks[b].ref_count == 1]
+        if max_blocks is not None:
+            todo = todo[:max_blocks]
+        if len(todo) > len(self.host_free):
+            raise RuntimeError(f"host swap pool has {len(self.host_free)} free slots, "
+                               f"{len(todo)} needed")
+        pairs, record = [], []
+        for i in todo:
+            slot = self.host_free.pop()
+            pairs.append((seq.block_table[i], slot))
+            record.append((i, slot))
+            bm.release(seq.block_table[i])
+            seq.block_table[i] = -1
+        self.swapped[seq.seq_id] = record
+        return pairs
+
+    def can_swap_in(self, seq: Sequence) -> bool:
+        return self.block_manager.num_free_blocks >= len(self.swapped.get(seq.seq_id, ()))
+
+    def swap_in(self, seq: Sequence) -> list[tuple[int, int]]:
+        """Give the sequence's swapped positions fresh device blocks.
+
+        Returns ``(host slot, device block)`` pairs to copy host -> device before the sequence runs.
+        """
+        record = self.swapped.pop(seq.seq_id, [])
+        if len(record) > self.block_manager.num_free_blocks:
+            self.swapped[seq.seq_id] = record
+            raise RuntimeError("not enough free device blocks to swap in")
+        pairs = []
+        for i, slot in record:
+            bid = self.block_manager.allocate_block()
+            seq.block_table[i] = bid
+            pairs.append((slot, bid))
+            self.host_free.append(slot)
+        return pairs
 
     def shares_blocks(self, seqs: list[Sequence]) -> bool:
         """Whether any block of these sequences is held by more than one sequence: the decode
         hint ``kv_reuse`` (shared pages are then worth keeping in cache)."""
         blocks = self.block_manager.blocks
-        return any(blocks[b].ref_count > 1 for s in seqs for b in s.block_table)
+        return any(b >= 0 and blocks[b].ref_count > 1 for s in seqs for b in s.block_table)
