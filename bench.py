@@ -189,6 +189,35 @@ def _time(fn, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) * 1e3 / steps
 
 
+def swap_config5(st, dev, args, layers: int = 16, fraction: float = 0.25) -> dict:
+    """Config 5's swap: a quarter of the sequences' unique blocks, K and V of all 16 layers, to
+    pinned host memory and back into fresh block ids, through one block-list launch each way."""
+    from tileinfer_amd.kernels.block_copy import swap_blocks
+
+    batch, width = st.block_table.shape
+    pool = st.k_cache.shape[0]
+    prefix_blocks = int((st.block_table == st.block_table[0:1]).all(dim=0).sum())
+    n_seq = int(batch * fraction)
+    unique = st.block_table[:n_seq, prefix_blocks:].reshape(-1).to(torch.int64)
+    n = unique.numel()
+    kv = torch.empty((2, layers, pool, BLOCK, HKV, HEAD_DIM), dtype=torch.bfloat16, device=dev)
+    kv.normal_(generator=torch.Generator(device=dev).manual_seed(11))
+    host = torch.empty((2, layers, n, BLOCK, HKV, HEAD_DIM), dtype=torch.bfloat16, pin_memory=True)
+    out_map = torch.stack([unique, torch.arange(n, device=dev)], dim=1)
+    # Swap back into other block ids (a reversed order of the same set stands in for fresh ids).
+    in_map = torch.stack([torch.arange(n, device=dev), unique.flip(0)], dim=1)
+    moved = 2 * layers * n * BLOCK * HKV * HEAD_DIM * 2
+    before = kv[:, :, unique].clone()
+    out_us = _time(lambda: swap_blocks(kv, host, out_map), max(2, args.steps // 4), 1)
+    in_us = _time(lambda: swap_blocks(host, kv, in_map), max(2, args.steps // 4), 1)
+    torch.cuda.synchronize()
+    ok = bool(torch.equal(kv[:, :, unique.flip(0)].view(torch.int16), before.view(torch.int16)))
+    return {"blocks": n, "layers": layers, "bytes_each_way": moved,
+            "swap_out_us": round(out_us, 1), "swap_out_GBps": round(moved / (out_us * 1e-6) / 1e9, 1),
+            "swap_in_us": round(in_us, 1), "swap_in_GBps": round(moved / (in_us * 1e-6) / 1e9, 1),
+            "roundtrip_bit_exact": ok, "bound": "host link (pinned host memory over the fabric)"}
+
+
 def run_config(cfg: int, args, dev) -> dict:
     """One attention layer of BASELINE config 1, 2, 4 or 5 (append, then decode), on the GPU."""
     from tileinfer_amd import workloads as wl
@@ -242,6 +271,7 @@ def run_config(cfg: int, args, dev) -> dict:
                                                       split_tokens=args.split_tokens,
                                                       variant=args.variant), args.steps, args.warmup)
         extra = {"decode_us_streaming_policy": round(stream_us, 2),
+                 "swap": swap_config5(st, dev, args),
                  "decode_logical_bytes": d_bytes,
                  "decode_physical_unique_kv_bytes": unique * 2 * BLOCK * HKV * HEAD_DIM * 2,
                  "note": "shared prefix blocks are re-read from L2/MALL, so the logical rate can "
