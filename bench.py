@@ -218,6 +218,44 @@ def swap_config5(st, dev, args, layers: int = 16, fraction: float = 0.25) -> dic
             "roundtrip_bit_exact": ok, "bound": "host link (pinned host memory over the fabric)"}
 
 
+def prefill_config4(st, chunk_slots, kc, vc, dev, args) -> dict:
+    """Config 4's 2048-token chunk through the paged prefill attention, straight from the cache
+    pages the append just wrote (first chunk: the chunk attends over itself), and a continuation
+    chunk of 2048 after 6144 cached tokens. Also timed: the reference recipe's torch gather of the
+    continuation's 8192 positions into contiguous K/V (model/qwen_36.py:1034-1044), which the
+    paged kernel does not need."""
+    from tileinfer_amd import workloads as wl
+    from tileinfer_amd.kernels.gqa_prefill_paged import gqa_prefill_paged_fn
+
+    chunk = chunk_slots.numel()
+    table = torch.tensor(st.meta["chunk_blocks"], dtype=torch.int32, device=dev).view(1, -1)
+    gen = torch.Generator(device=dev).manual_seed(6)
+    q = torch.randn((chunk, HQ, HEAD_DIM), generator=gen, device=dev).to(torch.bfloat16)
+    cu = torch.tensor([0, chunk], dtype=torch.int32, device=dev)
+    sk = torch.tensor([chunk], dtype=torch.int32, device=dev)
+    first_us = _time(lambda: gqa_prefill_paged_fn(q, kc, vc, table, cu, sk, chunk),
+                     args.steps, args.warmup)
+    first_flops = wl.prefill_flops([chunk], [chunk])
+    cont = wl.config4_prefill(device=dev, cached=6144, chunk=chunk)
+    cont_us = _time(lambda: gqa_prefill_paged_fn(cont.q, cont.k_cache, cont.v_cache,
+                                                 cont.block_table, cont.cu_seqlens_q,
+                                                 cont.seqlen_k, chunk), args.steps, args.warmup)
+    cont_flops = cont.flops()
+    kv_len = int(cont.seqlen_k[0])
+    pos = torch.arange(kv_len, device=dev)
+    blocks = cont.block_table[0, pos // BLOCK].long()
+    offs = pos % BLOCK
+    gather_us = _time(lambda: (cont.k_cache[blocks, offs].contiguous(),
+                               cont.v_cache[blocks, offs].contiguous()), args.steps, args.warmup)
+    tf = lambda f, us: round(f / (us * 1e-6) / 1e12, 1)  # noqa: E731
+    return {"first_chunk": {"q_len": chunk, "kv_len": chunk, "us": round(first_us, 2),
+                            "flops": first_flops, "TFLOPs": tf(first_flops, first_us)},
+            "continuation": {"q_len": chunk, "kv_len": kv_len, "us": round(cont_us, 2),
+                             "flops": cont_flops, "TFLOPs": tf(cont_flops, cont_us)},
+            "reference_gather_of_continuation_us": round(gather_us, 2),
+            "peak_TFLOPs_bf16_dense": 2500.0}
+
+
 def run_config(cfg: int, args, dev) -> dict:
     """One attention layer of BASELINE config 1, 2, 4 or 5 (append, then decode), on the GPU."""
     from tileinfer_amd import workloads as wl
@@ -264,7 +302,8 @@ def run_config(cfg: int, args, dev) -> dict:
         b_us = _time(lambda: store_kvcache(bk, bv, rows(kc), rows(vc), bs), args.steps, args.warmup)
         extra = {"append_two_calls_us": round(two, 2),
                  "append_bulk_65536_us": round(b_us, 2),
-                 "append_bulk_GBps_algorithmic": round(append_bytes(bs, HKV * HEAD_DIM) / (b_us * 1e-6) / 1e9, 1)}
+                 "append_bulk_GBps_algorithmic": round(append_bytes(bs, HKV * HEAD_DIM) / (b_us * 1e-6) / 1e9, 1),
+                 "prefill": prefill_config4(st, chunk_slots, kc, vc, dev, args)}
     if cfg == 5:
         unique = int(torch.unique(st.block_table).numel())
         stream_us = _time(lambda: gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen,

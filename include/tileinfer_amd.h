@@ -5,6 +5,9 @@
  *   - the slot-mapped K/V append           (replaces kernels/kvcache_store.py:43-71, store_kvcache)
  *   - single-query paged GQA decode        (replaces kernels/gqa_decode_paged.py:392-437,
  *     attention with a split-K merge         gqa_decode_paged_fn)
+ *   - block copies between caches           (swap out/in and copy-on-write; no reference kernel)
+ *   - paged causal GQA prefill attention    (replaces the gather + varlen flash attention of
+ *                                            model/qwen_36.py:1030-1065, kernels/gqa_varlen.py)
  *
  * Conventions shared by every entry point
  *   - All tensor pointers are DEVICE pointers owned by the caller. The library never allocates,
@@ -126,6 +129,37 @@ int ti_copy_blocks(const void* src, void* dst, const int64_t* block_pairs, int64
                    int32_t n_chunks, int64_t chunk_bytes, int64_t src_chunk_stride_bytes,
                    int64_t dst_chunk_stride_bytes, int64_t src_num_blocks, int64_t dst_num_blocks,
                    void* stream);
+
+/*
+ * Causal (or full) GQA prefill attention reading K/V straight from the paged cache.
+ *
+ * Replaces the chunked-prefill path of model/qwen_36.py:1030-1065, which gathers every cached
+ * position through block_tables into contiguous K/V and then calls the varlen flash-attention
+ * kernel kernels/gqa_varlen.py:40-185 (dispatch 369-389); same arguments' meaning, with the K/V
+ * source being the cache instead of the gathered copy. Sequence b owns query rows
+ * [cu_seqlens_q[b], cu_seqlens_q[b+1]) of `q` and attends over its first seqlen_k[b] cached tokens
+ * (the chunk's own K/V already appended), gathered through block_table[b]. With `causal` set the
+ * mask is bottom-right aligned (query i sees keys j <= seqlen_k[b] - q_len + i); query head h reads
+ * KV head h / (num_q_heads / num_kv_heads); scale = head_dim^-1/2; a row with no visible key is 0.
+ * Block ids outside [0, num_blocks) inside the context are absent pages (their keys are masked,
+ * never loaded); table entries past ceil(seqlen_k[b] / page_size) are never read.
+ *   q            [total_q, num_q_heads, head_dim] (16-byte aligned rows, unit innermost stride)
+ *   k/v_cache    as for ti_gqa_decode_paged
+ *   cu_seqlens_q [batch + 1] int32, non-decreasing, cu_seqlens_q[batch] <= total_q (values are
+ *                clamped into [0, total_q], so rows outside q/out are never touched)
+ *   seqlen_k     [batch] int32, clamped to max_blocks_per_seq * page_size
+ *   out          [total_q, num_q_heads, head_dim], written for every row covered by cu_seqlens_q
+ *   max_seqlen_q >= every q_len (rows past it are not computed)
+ * One launch on `stream`, no workspace. head_dim 128 or 256; page_size a multiple of 16.
+ */
+int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                         const void* k_cache, const void* v_cache, const int32_t* block_table,
+                         int64_t block_table_stride, const int32_t* cu_seqlens_q,
+                         const int32_t* seqlen_k, void* out, int64_t out_stride_t,
+                         int64_t out_stride_h, int32_t batch, int32_t total_q,
+                         int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
+                         int32_t head_dim, int32_t page_size, int64_t num_blocks,
+                         int32_t max_blocks_per_seq, int32_t causal, int32_t dtype, void* stream);
 
 /* Text of the last error reported on the calling thread ("" when none). */
 const char* ti_last_error(void);

@@ -92,3 +92,35 @@ def decode_loop_fp64(q, k_cache, v_cache, block_table, seqlen, page_size=16):
                 for e in range(d):
                     out[b][h][e] += ws[j] / tot * float(v_cache[blk][off][kvh][e])
     return out
+
+
+def prefill_fp64(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+                 block_table: np.ndarray, cu_seqlens_q: np.ndarray, seqlen_k: np.ndarray,
+                 page_size: int = 16, causal: bool = True) -> np.ndarray:
+    """float64 [total_q, H_q, D]: textbook softmax attention of every chunk query row.
+
+    Query i of sequence b (q_len rows, kv_len cached tokens) sits at absolute position
+    ``kv_len - q_len + i`` and, under ``causal``, sees keys ``0..kv_len - q_len + i``; a row that
+    sees no key is zero.
+    """
+    total_q, h_q, d = q.shape
+    h_kv = k_cache.shape[2]
+    g = h_q // h_kv
+    kf = np.asarray(k_cache, dtype=np.float64).reshape(-1, h_kv, d)
+    vf = np.asarray(v_cache, dtype=np.float64).reshape(-1, h_kv, d)
+    qf = np.asarray(q, dtype=np.float64)
+    out = np.zeros((total_q, h_q, d), dtype=np.float64)
+    for b in range(len(seqlen_k)):
+        q0, q1 = int(cu_seqlens_q[b]), int(cu_seqlens_q[b + 1])
+        kv_len = int(seqlen_k[b])
+        k = gather_context(kf, block_table[b], kv_len, page_size)
+        v = gather_context(vf, block_table[b], kv_len, page_size)
+        for i in range(q1 - q0):
+            visible = min(kv_len, kv_len - (q1 - q0) + i + 1) if causal else kv_len
+            if visible <= 0:
+                continue
+            for h in range(h_q):
+                s = k[:visible, h // g, :] @ qf[q0 + i, h] / math.sqrt(d)
+                w = np.exp(s - s.max())
+                out[q0 + i, h] = (w / w.sum()) @ v[:visible, h // g, :]
+    return out

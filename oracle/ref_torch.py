@@ -50,3 +50,56 @@ def ref_gqa_decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
             output[b, kv_h * groups:(kv_h + 1) * groups, :] = torch.matmul(weights,
                                                                             v_full[:, kv_h, :])
     return output
+
+
+def ref_gqa_prefill_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                          block_table: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                          seqlen_k: torch.Tensor, page_size: int = 16,
+                          causal: bool = True) -> torch.Tensor:
+    """[total_q, H_q, D] chunked-prefill attention of the reference recipe.
+
+    Gather: model/qwen_36.py:1034-1044 — positions ``0..kv_len-1`` of sequence b through
+    ``block_table[b]`` (``positions // page_size`` into the table, ``positions % page_size`` in
+    the page). Math: kernels/gqa_varlen.py:88-175 with one key tile covering the whole context —
+    ``S = Q K^T`` in fp32 from the input dtype, keys ``j > kv_len - q_len + i`` masked to -inf
+    under ``causal`` (120-131), ``P = exp2(S·scale - max·scale)`` with ``scale = D^-1/2 log2 e``
+    (44, 150-154), ``l = sum(P)`` in fp32 (155-157), ``P`` rounded to the input dtype before
+    ``P @ V`` (160-162), ``O = acc / l`` rounded to the input dtype, 0 where ``l == 0``
+    (166-175). The kernel's online softmax over 16/64-key tiles rounds P relative to the running
+    maximum instead, a difference well inside the bf16 tolerance.
+    """
+    total_q, h_q, d = q.shape
+    h_kv = k_cache.shape[2]
+    groups = h_q // h_kv
+    scale = (1.0 / d) ** 0.5 * 1.44269504
+    out = torch.zeros(total_q, h_q, d, dtype=q.dtype, device=q.device)
+    k_flat = k_cache.reshape(-1, h_kv, d)
+    v_flat = v_cache.reshape(-1, h_kv, d)
+    cu = cu_seqlens_q.tolist()
+    for b in range(block_table.shape[0]):
+        q0, q1 = cu[b], cu[b + 1]
+        q_len = q1 - q0
+        kv_len = int(seqlen_k[b].item())
+        if q_len <= 0:
+            continue
+        positions = torch.arange(kv_len)
+        rows = block_table[b, positions // page_size].long() * page_size + positions % page_size
+        k_full = k_flat[rows]
+        v_full = v_flat[rows]
+        offset = kv_len - q_len
+        qi = torch.arange(q_len).unsqueeze(1)
+        kj = torch.arange(kv_len).unsqueeze(0)
+        masked = (qi + offset < kj) if causal else torch.zeros(q_len, kv_len, dtype=torch.bool)
+        for h in range(h_q):
+            kvh = h // groups
+            s = q[q0:q1, h, :].float() @ k_full[:, kvh, :].float().T
+            s = s.masked_fill(masked, float("-inf"))
+            m = s.max(dim=1, keepdim=True).values if kv_len else torch.full((q_len, 1), -torch.inf)
+            m_use = torch.where(torch.isinf(m), torch.zeros_like(m), m)
+            p = torch.exp2(s * scale - m_use * scale)
+            l = p.sum(dim=1, keepdim=True)
+            acc = p.to(q.dtype).float() @ v_full[:, kvh, :].float()
+            o = torch.where(l > 0, acc / torch.where(l > 0, l, torch.ones_like(l)),
+                            torch.zeros_like(acc))
+            out[q0:q1, h, :] = o.to(q.dtype)
+    return out

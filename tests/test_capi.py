@@ -9,6 +9,7 @@ import torch
 
 from tileinfer_amd import _lib
 from tileinfer_amd.kernels.gqa_decode_paged import gqa_decode_paged_fn
+from tileinfer_amd.kernels.gqa_prefill_paged import gqa_prefill_paged_fn
 from tileinfer_amd.kernels.kvcache_store import store_kvcache
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "tileinfer_amd.h"
@@ -96,6 +97,32 @@ def test_python_wrappers_validate_before_launch():
         gqa_decode_paged_fn(q, kc, kc, bt, sl, page_size=24)
     with pytest.raises(ValueError, match="GPU"):
         gqa_decode_paged_fn(q, kc, kc, bt, sl)
+    cu = torch.tensor([0, 1, 2], dtype=torch.int32)
+    with pytest.raises(TypeError):
+        gqa_prefill_paged_fn(q, kc, kc, bt, cu.long(), sl)
+    with pytest.raises(ValueError):
+        gqa_prefill_paged_fn(q, kc, kc, bt, cu[:2], sl)
+    with pytest.raises(ValueError):
+        gqa_prefill_paged_fn(q, kc, kc, bt, cu, sl, 1, page_size=24)
+    with pytest.raises(ValueError, match="GPU"):
+        gqa_prefill_paged_fn(q, kc, kc, bt, cu, sl, 1)
+
+
+def _prefill_abi(batch=1, total_q=4, max_q=4, hq=24, hkv=4, d=256, ps=16, dtype=0, ptr=None):
+    lib = _lib.load()
+    return lib.ti_gqa_prefill_paged(ptr, 24 * d, d, ptr, ptr, ptr, 8, ptr, ptr, ptr, 24 * d, d,
+                                    batch, total_q, max_q, hq, hkv, d, ps, 64, 8, 1, dtype, None)
+
+
+def test_prefill_argument_errors_without_device():
+    assert _prefill_abi(batch=0) == _lib.TI_OK
+    assert _prefill_abi(total_q=0) == _lib.TI_OK
+    assert _prefill_abi(dtype=7) == _lib.TI_EUNSUPPORTED
+    assert _prefill_abi(d=96) == _lib.TI_EUNSUPPORTED
+    assert _prefill_abi(ps=8) == _lib.TI_EUNSUPPORTED
+    assert _prefill_abi(hq=25) == _lib.TI_EINVAL
+    rc = _prefill_abi()
+    assert rc == _lib.TI_EINVAL and b"null" in _lib.load().ti_last_error()
 
 
 def test_missing_library_fails_loudly(tmp_path):

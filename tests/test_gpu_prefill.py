@@ -1,0 +1,195 @@
+"""Parity of the HIP paged prefill attention (ti_gqa_prefill_paged) with the CPU oracle, and the
+bitwise properties of the kernel at full size: a chunked prefill equals the one-shot prefill of
+the same tokens, shared prefix pages equal private copies, physical placement does not matter."""
+import pytest
+import torch
+
+from helpers import ATOL, RTOL, bits, say
+from oracle.brute import prefill_fp64
+from oracle.ref_torch import ref_gqa_prefill_paged
+from tileinfer_amd.kernels.gqa_decode_paged import gqa_decode_paged_fn
+from tileinfer_amd.kernels.gqa_prefill_paged import gqa_prefill_paged_fn
+from tileinfer_amd.workloads import config4_prefill, prefill_step
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gpu(step, dev, causal=True, **kw):
+    return gqa_prefill_paged_fn(step.q.to(dev), step.k_cache.to(dev), step.v_cache.to(dev),
+                                step.block_table.to(dev), step.cu_seqlens_q.to(dev),
+                                step.seqlen_k.to(dev), step.max_seqlen_q, step.page_size,
+                                causal=causal, **kw)
+
+
+def run_ref(step, causal=True):
+    return ref_gqa_prefill_paged(step.q, step.k_cache, step.v_cache, step.block_table,
+                                 step.cu_seqlens_q, step.seqlen_k, step.page_size, causal)
+
+
+def close(out, ref, atol=ATOL, rtol=RTOL):
+    torch.testing.assert_close(out.float().cpu(), ref.float().cpu(), atol=atol, rtol=rtol)
+
+
+@pytest.mark.parametrize("q_lens,kv_lens", [
+    ([64], [64]),                        # one full workgroup, first chunk
+    ([100], [100]),                      # ragged last workgroup
+    ([37], [300]),                       # continuation: 263 cached tokens before the chunk
+    ([16, 1, 0, 50, 129], [16, 200, 5, 51, 1000]),   # ragged batch, an empty chunk
+    ([1], [1]), ([3], [2000]),
+])
+def test_vs_oracle(q_lens, kv_lens, dev):
+    say(f"prefill q_lens={q_lens} kv_lens={kv_lens}")
+    step = prefill_step(q_lens, kv_lens, seed=21)
+    out = run_gpu(step, dev)
+    close(out, run_ref(step))
+    exact = torch.from_numpy(prefill_fp64(
+        step.q.double().numpy(), step.k_cache.double().numpy(), step.v_cache.double().numpy(),
+        step.block_table.numpy(), step.cu_seqlens_q.numpy(), step.seqlen_k.numpy()))
+    close(out, exact)
+
+
+def test_noncausal_vs_oracle(dev):
+    say("prefill non-causal")
+    step = prefill_step([40, 70], [90, 70], seed=22)
+    close(run_gpu(step, dev, causal=False), run_ref(step, causal=False))
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype", [
+    (24, 4, 256, torch.float16), (32, 4, 128, torch.bfloat16), (8, 8, 128, torch.float16),
+    (16, 1, 256, torch.bfloat16)])
+def test_shapes_and_dtypes(hq, hkv, d, dtype, dev):
+    say(f"prefill hq={hq} hkv={hkv} d={d} dtype={dtype}")
+    step = prefill_step([70, 19], [130, 19], seed=23, hq=hq, hkv=hkv, d=d, dtype=dtype)
+    close(run_gpu(step, dev), run_ref(step))
+
+
+def test_config4_first_chunk_vs_oracle(dev):
+    """Config 4's 2048-token chunk over its 128 non-contiguous blocks, against the oracle."""
+    step = config4_prefill()
+    say("prefill config4 chunk 2048 (first chunk)")
+    close(run_gpu(step, dev), run_ref(step))
+
+
+def test_chunked_equals_one_shot_bitwise(dev):
+    """A 4096-token prompt prefilled in chunks of 1000/1000/2000/96 tokens gives bitwise the
+    rows of the one-shot prefill: key tiles sit at absolute positions and masked keys add
+    exact zeros, so no result depends on how the prompt was chunked."""
+    say("prefill chunked vs one-shot, 4096 tokens")
+    full = prefill_step([4096], [4096], seed=24)
+    q = full.q.to(dev)
+    kc, vc = full.k_cache.to(dev), full.v_cache.to(dev)
+    bt = full.block_table.to(dev)
+    one = gqa_prefill_paged_fn(q, kc, vc, bt, full.cu_seqlens_q.to(dev), full.seqlen_k.to(dev),
+                               4096)
+    start = 0
+    for n in (1000, 1000, 2000, 96):
+        cu = torch.tensor([0, n], dtype=torch.int32, device=dev)
+        sk = torch.tensor([start + n], dtype=torch.int32, device=dev)
+        part = gqa_prefill_paged_fn(q[start:start + n], kc, vc, bt, cu, sk, n)
+        assert torch.equal(bits(part), bits(one[start:start + n])), f"chunk at {start}"
+        start += n
+
+
+def test_batched_equals_separate_bitwise(dev):
+    """Several sequences in one launch give bitwise what each gives alone."""
+    say("prefill batched vs separate")
+    step = prefill_step([300, 64, 5], [900, 64, 700], seed=25)
+    dq = step.q.to(dev)
+    kc, vc = step.k_cache.to(dev), step.v_cache.to(dev)
+    bt = step.block_table.to(dev)
+    together = run_gpu(step, dev)
+    cu = step.cu_seqlens_q.tolist()
+    for b in range(3):
+        alone = gqa_prefill_paged_fn(
+            dq[cu[b]:cu[b + 1]], kc, vc, bt[b:b + 1],
+            torch.tensor([0, cu[b + 1] - cu[b]], dtype=torch.int32, device=dev),
+            step.seqlen_k[b:b + 1].to(dev))
+        assert torch.equal(bits(alone), bits(together[cu[b]:cu[b + 1]]))
+
+
+def test_shared_prefix_equals_private_bitwise(dev):
+    """Two sequences whose tables alias one cached prefix, against private copies of it."""
+    say("prefill shared vs private prefix")
+    pre, chunk, bs = 512, 200, 16
+    base = prefill_step([chunk, chunk], [pre + chunk, pre + chunk], seed=26)
+    pb = pre // bs
+    shared_bt = base.block_table.clone()
+    shared_bt[1, :pb] = shared_bt[0, :pb]            # sequence 1 aliases sequence 0's prefix
+    kc, vc = base.k_cache.clone(), base.v_cache.clone()
+    private = base.block_table
+    for j in range(pb):                               # make the private copies equal in value
+        kc[private[1, j]] = kc[private[0, j]]
+        vc[private[1, j]] = vc[private[0, j]]
+    args = (base.q.to(dev), kc.to(dev), vc.to(dev))
+    tail = (base.cu_seqlens_q.to(dev), base.seqlen_k.to(dev), chunk)
+    a = gqa_prefill_paged_fn(*args, shared_bt.to(dev), *tail)
+    b = gqa_prefill_paged_fn(*args, private.to(dev), *tail)
+    assert torch.equal(bits(a), bits(b))
+
+
+def test_last_row_matches_decode(dev):
+    """The chunk's last query sees the whole context: the same value as a decode of that query
+    (two different kernels; within the decode tolerance)."""
+    say("prefill last row vs decode kernel")
+    step = prefill_step([128], [3000], seed=27)
+    out = run_gpu(step, dev)
+    dec = gqa_decode_paged_fn(step.q[-1:].to(dev), step.k_cache.to(dev), step.v_cache.to(dev),
+                              step.block_table.to(dev), step.seqlen_k.to(dev))
+    close(out[-1:], dec)
+
+
+def test_empty_contexts_give_zeros_and_rows_outside_untouched(dev):
+    """kv_len 0 gives zeros; rows with no visible key (kv_len < q_len) give zeros; rows outside
+    every chunk (past cu_seqlens_q[-1]) keep what the caller's buffer held."""
+    say("prefill zero rows and untouched rows")
+    step = prefill_step([4, 6], [0, 3], seed=28)
+    q = torch.cat([step.q, torch.randn(5, 24, 256).to(torch.bfloat16)]).to(dev)
+    out = torch.full((q.shape[0], 24, 256), 7.0, dtype=torch.bfloat16, device=dev)
+    gqa_prefill_paged_fn(q, step.k_cache.to(dev), step.v_cache.to(dev), step.block_table.to(dev),
+                         step.cu_seqlens_q.to(dev), step.seqlen_k.to(dev), 6, out=out)
+    o = out.float().cpu()
+    assert (o[:4] == 0).all()                 # kv_len 0
+    assert (o[4:7] == 0).all()                # offset -3: rows 0..2 see nothing
+    assert (o[7:10] != 0).any()
+    close(o[4:10], run_ref(step)[4:10])
+    assert (o[10:] == 7.0).all()
+
+
+def test_out_of_range_block_ids_are_masked(dev):
+    """A block id outside the cache inside the context is an absent page: its 16 keys are masked
+    (never read); -1 padding past the context is ignored."""
+    say("prefill bad block ids")
+    step = prefill_step([20], [40], seed=29, width=6)
+    bt = step.block_table.clone()
+    bt[0, 1] = 10 ** 8                        # keys 16..31 live in a block that does not exist
+    out = gqa_prefill_paged_fn(step.q.to(dev), step.k_cache.to(dev), step.v_cache.to(dev),
+                               bt.to(dev), step.cu_seqlens_q.to(dev), step.seqlen_k.to(dev))
+    # Expected: float64 attention of each row over its visible keys minus 16..31.
+    kf = step.k_cache.double().reshape(-1, 4, 256)
+    vf = step.v_cache.double().reshape(-1, 4, 256)
+    rows = [int(step.block_table[0, j // 16]) * 16 + j % 16 for j in range(40)]
+    k, v = kf[rows], vf[rows]
+    want = torch.zeros(20, 24, 256, dtype=torch.float64)
+    for i in range(20):
+        keys = [j for j in range(20 + i + 1) if not 16 <= j < 32]
+        for h in range(24):
+            s = k[keys, h // 6] @ step.q[i, h].double() / 16.0
+            want[i, h] = torch.softmax(s, 0) @ v[keys, h // 6]
+    close(out, want)
+
+
+def test_rejects_bad_arguments(dev):
+    step = prefill_step([8], [8], seed=30)
+    q, kc, vc = step.q.to(dev), step.k_cache.to(dev), step.v_cache.to(dev)
+    bt, cu, sk = step.block_table.to(dev), step.cu_seqlens_q.to(dev), step.seqlen_k.to(dev)
+    with pytest.raises(TypeError):
+        gqa_prefill_paged_fn(q, kc, vc, bt.long(), cu, sk)
+    with pytest.raises(ValueError):
+        gqa_prefill_paged_fn(q, kc, vc, bt, cu[:1], sk)
+    with pytest.raises(ValueError):
+        gqa_prefill_paged_fn(q, kc, vc, bt, cu, sk, page_size=24)
+    from tileinfer_amd._lib import TileInferError
+    q96 = torch.zeros(8, 24, 96, dtype=torch.bfloat16, device=dev)
+    k96 = torch.zeros(kc.shape[0], 16, 4, 96, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(TileInferError):
+        gqa_prefill_paged_fn(q96, k96, k96, bt, cu, sk)

@@ -203,3 +203,75 @@ def config5(seed: int = 1005, device="cpu", batch: int = 128, prefix: int = 8192
                      block_table=table, seqlen=torch.tensor(ctx, dtype=torch.int32, device=device),
                      k_cache=k_cache, v_cache=v_cache,
                      meta={"seed": seed, "ctx": ctx, "shared": shared})
+
+
+@dataclass
+class PrefillStep:
+    """One attention layer's chunked-prefill inputs: packed query rows over paged K/V.
+
+    Sequence b owns query rows ``cu_seqlens_q[b]:cu_seqlens_q[b+1]`` (its chunk) and has
+    ``seqlen_k[b]`` tokens in the cache, the chunk's own K/V included (already appended).
+    """
+    q: torch.Tensor             # [total_q, HQ, D]
+    block_table: torch.Tensor   # [B, W] int32, -1 padded
+    cu_seqlens_q: torch.Tensor  # [B + 1] int32
+    seqlen_k: torch.Tensor      # [B] int32
+    k_cache: torch.Tensor       # [num_blocks, BLOCK, HKV, D]
+    v_cache: torch.Tensor
+    max_seqlen_q: int = 0
+    page_size: int = BLOCK
+    meta: dict = field(default_factory=dict)
+
+    def flops(self) -> int:
+        return prefill_flops(self.q_lens(), self.seqlen_k.tolist(), self.q.shape[1],
+                             self.q.shape[2])
+
+    def q_lens(self) -> list[int]:
+        cu = self.cu_seqlens_q.tolist()
+        return [cu[i + 1] - cu[i] for i in range(len(cu) - 1)]
+
+
+def prefill_visible(q_len: int, kv_len: int, causal: bool = True) -> int:
+    """Number of (query, key) pairs a chunk attends over: query i sees keys
+    ``0..kv_len - q_len + i`` under the bottom-right causal mask."""
+    if not causal:
+        return q_len * kv_len
+    off = kv_len - q_len
+    return sum(max(0, min(kv_len, off + i + 1)) for i in range(q_len))
+
+
+def prefill_flops(q_lens: list[int], kv_lens: list[int], hq: int = HQ, d: int = HEAD_DIM,
+                  causal: bool = True) -> int:
+    """Algorithmic flops of the chunks' attention: 2·D for Q·K and 2·D for P·V per visible pair."""
+    return 4 * hq * d * sum(prefill_visible(a, b, causal) for a, b in zip(q_lens, kv_lens))
+
+
+def prefill_step(q_lens: list[int], kv_lens: list[int], seed: int, device="cpu",
+                 pool: int | None = None, dtype=torch.bfloat16, value_scale: float = 1.0,
+                 hq: int = HQ, hkv: int = HKV, d: int = HEAD_DIM,
+                 width: int | None = None) -> PrefillStep:
+    """Random non-contiguous tables from a pool (1.25x the need by default), N(0,1)·scale values."""
+    if len(q_lens) != len(kv_lens):
+        raise ValueError("q_lens and kv_lens differ in length")
+    need = sum((c + BLOCK - 1) // BLOCK for c in kv_lens)
+    pool = max(1, math.ceil(1.25 * need)) if pool is None else pool
+    gen = torch.Generator(device=device).manual_seed(seed)
+    table = tables_from_pool(kv_lens, pool, gen, device, width)
+    k_cache = _randn((pool, BLOCK, hkv, d), gen, device, dtype, value_scale)
+    v_cache = _randn((pool, BLOCK, hkv, d), gen, device, dtype, value_scale)
+    cu = [0]
+    for n in q_lens:
+        cu.append(cu[-1] + n)
+    q = _randn((cu[-1], hq, d), gen, device, dtype, value_scale)
+    return PrefillStep(q=q, block_table=table,
+                       cu_seqlens_q=torch.tensor(cu, dtype=torch.int32, device=device),
+                       seqlen_k=torch.tensor(kv_lens, dtype=torch.int32, device=device),
+                       k_cache=k_cache, v_cache=v_cache, max_seqlen_q=max(q_lens, default=0),
+                       meta={"seed": seed, "q_lens": list(q_lens), "kv_lens": list(kv_lens)})
+
+
+def config4_prefill(seed: int = 1004, device="cpu", chunk: int = 2048,
+                    cached: int = 0) -> PrefillStep:
+    """Config 4's prefill chunk as attention input: ``chunk`` query tokens over ``cached + chunk``
+    tokens held in random non-contiguous blocks (``cached = 0``: the first chunk, 128 blocks)."""
+    return prefill_step([chunk], [cached + chunk], seed, device)
