@@ -13,30 +13,18 @@
 // sees all kv_len keys), the reference's is_causal=False. As in the decode kernel, a block id
 // outside [0, num_blocks) inside the context is an absent page: its keys are masked, never loaded.
 //
-// Work unit: a workgroup = 64 query tokens of one query head (4 waves x 16 tokens); 32-key tiles of
-// that head's KV head are staged in LDS (prefetched into registers one tile ahead, one barrier per
-// tile) straight from the pages. Each wave uses the decode kernel's transposed MFMA layout with its
-// 16 query tokens as the 16 columns:
-//   S^T[16 keys x 16 queries] = K[16 keys x 32 d] . Q^T[32 d x 16 queries]    (16x16x32)
-//   O^T[16 d x 16 queries]   += V^T[16 d x 16 keys] . P^T[16 keys x 16 queries] (16x16x16)
-// so every accumulator's query is its lane's column and the softmax rescale stays in the lane.
+// Work unit: a workgroup = one (sequence, KV head, block of query tokens), whose rows are the
+// (token, query head) pairs of the KV head's group, so each 32-key K/V tile staged in LDS is shared
+// by every query head of the group (GQA packing) and each K/V operand read from LDS feeds C MFMAs
+// (C column tiles of 16 rows per wave). Tiles are loaded straight from the pages one tile ahead,
+// through per-page buffer descriptors. Each wave uses the transposed MFMA layout:
+//   S^T[16 keys x 16 rows]  = K[16 keys x 32 d] . Q^T[32 d x 16 rows]       (16x16x32, D/32 steps)
+//   O^T[16 d x 16 rows]    += V^T[16 d x 32 keys] . P^T[32 keys x 16 rows]   (16x16x32)
+// so each accumulator's query row is its lane's column and the softmax stays inside the lane.
 #include "decode_common.h"
 
 namespace ti {
 namespace {
-
-typedef __bf16 pf_bf16x4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 pf_f16x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c, Bf16) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(pf_bf16x4_t, a),
-                                                   __builtin_bit_cast(pf_bf16x4_t, b), c, 0, 0, 0);
-}
-__device__ __forceinline__ f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c, F16) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(pf_f16x4_t, a),
-                                               __builtin_bit_cast(pf_f16x4_t, b), c, 0, 0, 0);
-}
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -51,200 +39,338 @@ struct PrefillArgs {
   uint16_t* out;
   int64_t o_st, o_sh;
   int32_t total_q, num_blocks32, hq, hkv, group, page_size, max_blocks, causal;
+  int32_t tq;  // query tokens per workgroup: floor(64 * C / group)
   float scale_log2;
 };
 
-constexpr int kQB = 64;   // query tokens per workgroup
-constexpr int kKT = 32;   // keys per staged tile
+constexpr int kKT = 32;  // keys per staged tile (two 16-key sub-tiles, each inside one page)
+constexpr float kRescaleSlack = 8.f;  // exp2 units a row maximum may rise before O is rescaled
 
-template <int D, typename Tag>
-__global__ __launch_bounds__(256) void prefill_mfma_kernel(PrefillArgs a) {
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// LDS slot of 16-byte chunk c of K/V tile row r is c ^ lds_swizzle(r). On gfx950 a ds_read_b128
+// serves 16 lanes per cycle over 64 banks: lanes {0-3, 12-15, 20-23, 24-27} together, then
+// {4-11, 16-19, 28-31}, and the same for lanes 32-63 (measured with SQ_LDS_BANK_CONFLICT). With
+// this swizzle both MFMA operand reads of the tile -- K rows across lanes, V rows across
+// 16-lane groups -- hit 16 distinct bank quads per cycle, for head_dim 128 and 256.
+__device__ __forceinline__ int lds_swizzle(int r) { return (r ^ ((r << 1) & 8)) & 15; }
+
+// Max over the four 16-lane rows of the wave (lanes n, n+16, n+32, n+48).
+__device__ __forceinline__ float row_group_max(float x) {
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float row_group_sum(float x) {
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// One workgroup = one (sequence, KV head, block of tq query tokens); its rows are the
+// (token, query head) pairs of that KV head's group, row = token * group + head-in-group, 64*C rows
+// over 4 waves (C column tiles of 16 rows per wave). Every staged K/V tile is thus shared by all
+// query heads of the group, and every K/V operand read from LDS feeds C MFMAs.
+//
+// K/V tiles go from the pages straight into LDS (buffer loads with the LDS destination), two
+// stages in distinct arrays so that the compiler's wait counting tells the stage being loaded from
+// the stage being read. LDS rows are unpadded and swizzled (lds_swizzle) so that the MFMA operand
+// reads are free of bank conflicts.
+template <int D, int C, int W, typename Tag>
+__global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int KK = D / 32;
   constexpr int NC = D / 128;
   constexpr int NT = D / 16;
-  constexpr int ROW = D + 8;                 // padded LDS row (16-bit elements)
-  constexpr int CPR = D / 8;                 // 16-byte chunks per row
-  constexpr int CPT = kKT * CPR / 256;       // chunks per thread per tile, each of K and V
-  static_assert(CPT * 256 == kKT * CPR, "tile must split evenly over 256 lanes");
+  constexpr int CPR = D / 8;              // 16-byte chunks per row
+  constexpr int RPB = 1024 / (2 * D);     // rows per 1 KiB load (64 lanes x 16 bytes)
+  constexpr int LPW = kKT / RPB / W;      // 1 KiB loads per wave per tile, each of K and V
+  static_assert(LPW * RPB * W == kKT && 16 % RPB == 0, "loads must not straddle sub-tiles");
 
-  __shared__ __align__(16) uint16_t sk[2][kKT * ROW];
-  __shared__ __align__(16) uint16_t sv[2][kKT * ROW];
-  // Key j of the staged tile exists (inside the context, with a block id inside the cache): the
-  // byte s_ok[buf][j] is 1. Keys that do not exist are masked out, like the decode kernel's.
-  __shared__ __align__(4) uint8_t s_ok[2][kKT];
+  __shared__ __align__(1024) uint16_t sk0[kKT * D];
+  __shared__ __align__(1024) uint16_t sv0[kKT * D];
+  __shared__ __align__(1024) uint16_t sk1[kKT * D];
+  __shared__ __align__(1024) uint16_t sv1[kKT * D];
 
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int n = lane & 15;  // query column of S^T/O^T; key row of K; d-column of V^T
+  const int n = lane & 15;
   const int g = lane >> 4;
-  const int h = blockIdx.y;
+  const int kvh = blockIdx.x;
   const int b = blockIdx.z;
-  const int kvh = h / a.group;
+  const int G = a.group;
 
-  // Row ranges are clamped into [0, total_q): a malformed cu_seqlens_q cannot move an access
-  // outside q/out.
   const int q_start = min(max(a.cu_q[b], 0), a.total_q);
   const int q_len = min(max(a.cu_q[b + 1], q_start), a.total_q) - q_start;
-  const int qb0 = blockIdx.x * kQB;
+  // Heaviest query blocks (latest tokens, longest causal range) are dispatched first.
+  const int qb0 = (gridDim.y - 1 - blockIdx.y) * a.tq;
   if (qb0 >= q_len) return;  // uniform over the workgroup
   int kv_len = a.seqlen_k[b];
   const int cap = a.max_blocks * a.page_size;
   kv_len = kv_len < 0 ? 0 : (kv_len > cap ? cap : kv_len);
   const int offset = kv_len - q_len;  // query i sits at absolute position offset + i
+  const int tq = min(a.tq, q_len - qb0);
 
-  const int q0 = qb0 + 16 * wave;        // this wave's first query token
-  const bool row_ok = q0 + n < q_len;
-  const int q_pos = offset + q0 + n;     // absolute position of this lane's query
-
-  // Q^T operand of this lane's query row (zero for rows past the chunk).
-  u32x4 qop[KK];
-  {
-    const uint16_t* qrow = a.q + int64_t(q_start + q0 + n) * a.q_st + int64_t(h) * a.q_sh;
+  // This lane's C rows.
+  bool row_ok[C];
+  int q_pos[C];
+  u32x4 qop[C][KK];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int rho = wave * 16 * C + 16 * c + n;
+    const int tok = rho / G;
+    const int hh = rho - tok * G;
+    row_ok[c] = tok < tq;
+    q_pos[c] = a.causal ? offset + qb0 + tok : INT32_MAX;
+    const uint16_t* qrow =
+        a.q + int64_t(q_start + qb0 + tok) * a.q_st + int64_t(kvh * G + hh) * a.q_sh + 8 * g;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      qop[kk] = row_ok ? load16(qrow + 32 * kk + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+      qop[c][kk] = row_ok[c] ? load16(qrow + 32 * kk) : u32x4{0u, 0u, 0u, 0u};
     }
   }
 
-  f32x4 o[NT];
+  f32x4 o[C][NT];
+  float m_run[C], l_run[C];
 #pragma unroll
-  for (int i = 0; i < NT; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;
-  float l_run = 0.f;
+  for (int c = 0; c < C; ++c) {
+#pragma unroll
+    for (int i = 0; i < NT; ++i) o[c][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run[c] = -INFINITY;
+    l_run[c] = 0.f;
+  }
 
-  // Keys the workgroup can see: j < kv_len, and j < offset + qb0 + kQB under the causal mask.
-  int k_end = a.causal ? min(kv_len, offset + qb0 + kQB) : kv_len;
+  // Keys the workgroup can see: j < kv_len, and j < offset + qb0 + tq under the causal mask.
+  int k_end = a.causal ? min(kv_len, offset + qb0 + tq) : kv_len;
   if (k_end < 0) k_end = 0;
   const int ntiles = (k_end + kKT - 1) / kKT;
   // Under the causal mask, keys past this one are masked for every row of the wave.
-  const int wave_last_key = a.causal ? offset + q0 + 15 : INT32_MAX;
+  const int wave_tok = min(tq - 1, ((wave + 1) * 16 * C - 1) / G);
+  const int wave_last_key = a.causal ? offset + qb0 + wave_tok : INT32_MAX;
+  // Keys up to this one are visible to every row of the wave.
+  const int wave_first_key = a.causal ? offset + qb0 + (wave * 16 * C) / G : INT32_MAX;
 
-  u32x4 pk[CPT], pv[CPT];
-  uint32_t pok = 0;  // bit j: chunk j's key exists
-  auto fetch = [&](int k0) {
-    pok = 0;
+  const uint32_t row_bytes = uint32_t(a.row_stride) * 2u;
+  const int32_t* bt_row = a.block_table + int64_t(b) * a.bt_stride;
+
+  // Block ids of the next tile to load (uniform), fetched one tile ahead of their use.
+  int nbid[2], nrows[2];
+  auto load_ids = [&](int k0) {
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      const int ci = t + 256 * j;
-      const int r = ci / CPR, col = ci % CPR;
-      const int key = k0 + r;
-      int bid = -1;
-      if (key < kv_len) {
-        bid = a.block_table[int64_t(b) * a.bt_stride + key / a.page_size];
-        if (uint32_t(bid) >= uint32_t(a.num_blocks32)) bid = -1;
+    for (int sub = 0; sub < 2; ++sub) {
+      const int key0 = k0 + 16 * sub;
+      int rows = min(max(kv_len - key0, 0), 16);
+      const int id = rows > 0 ? bt_row[key0 / a.page_size] : 0;
+      nbid[sub] = id;
+      nrows[sub] = rows;
+    }
+  };
+  // Rows of each sub-tile that exist in the two stages (uniform).
+  int rows_st[2][2];
+  // Issue the loads of the tile at key k0 into stage (sk, sv). A sub-tile lies in one page; its
+  // loads use a buffer descriptor spanning only the rows that exist, so rows past the context or
+  // in an absent page land in LDS as zero without a memory access.
+  auto fetch = [&](uint16_t* sk, uint16_t* sv, int (&rows_out)[2], int k0) {
+    __amdgpu_buffer_rsrc_t rk[2], rv[2];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      int rows = nrows[sub];
+      int bid = nbid[sub];
+      if (uint32_t(bid) >= uint32_t(a.num_blocks32)) {
+        rows = 0;
+        bid = 0;
       }
-      if (bid >= 0) {
-        const int64_t off = int64_t(bid) * a.page_stride + int64_t(key % a.page_size) * a.row_stride +
-                            int64_t(kvh) * D + 8 * col;
-        pk[j] = load16(a.k_cache + off);
-        pv[j] = load16(a.v_cache + off);
-        pok |= 1u << j;
+      bid = __builtin_amdgcn_readfirstlane(bid);
+      rows = __builtin_amdgcn_readfirstlane(rows);
+      const int key0 = k0 + 16 * sub;
+      const int64_t base = int64_t(bid) * a.page_stride +
+                           int64_t(key0 % a.page_size) * a.row_stride + int64_t(kvh) * D;
+      const uint32_t nbytes = rows > 0 ? uint32_t(rows - 1) * row_bytes + D * 2 : 0u;
+      rk[sub] = make_rsrc(a.k_cache + base, nbytes);
+      rv[sub] = make_rsrc(a.v_cache + base, nbytes);
+      rows_out[sub] = rows;
+    }
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int blk = wave * LPW + i;                  // 1 KiB block of the tile (uniform)
+      const int row = blk * RPB + lane / CPR;          // tile row of this lane's chunk
+      const int slot = lane % CPR;
+      const int chunk = slot ^ lds_swizzle(row);
+      const uint32_t off = uint32_t(row & 15) * row_bytes + uint32_t(chunk) * 16u;
+      const int sub = (blk * RPB) / 16;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sub ? rk[1] : rk[0], (lds_ptr_t)(sk + blk * 512),
+                                               16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sub ? rv[1] : rv[0], (lds_ptr_t)(sv + blk * 512),
+                                               16, off, 0, 0, 0);
+    }
+  };
+
+  auto compute = [&](const uint16_t* sk, const uint16_t* sv, const int (&rows)[2], int k0) {
+    const bool do1 = k0 + 16 <= wave_last_key;  // sub-tile 1 holds a key some row can see
+    f32x4 s0[C], s1[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      s0[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      s1[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    {
+      u32x4 kop[KK];
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        kop[kk] = *reinterpret_cast<const u32x4*>(sk + n * D + (((4 * kk + g) ^ lds_swizzle(n)) * 8));
+      }
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) s0[c] = mfma16x16x32(kop[kk], qop[c][kk], s0[c], Tag{});
+      }
+    }
+    if (do1) {
+      u32x4 kop[KK];
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        kop[kk] =
+            *reinterpret_cast<const u32x4*>(sk + (16 + n) * D + (((4 * kk + g) ^ lds_swizzle(n)) * 8));
+      }
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) s1[c] = mfma16x16x32(kop[kk], qop[c][kk], s1[c], Tag{});
+      }
+    }
+    const int rows0 = rows[0];
+    const int rows1 = do1 ? rows[1] : 0;
+    // A tile wholly below the wave's diagonal with all 32 keys present needs no mask (uniform).
+    const bool full = (rows0 == 16) & (rows1 == 16) & (k0 + 31 <= wave_first_key);
+    u32x4 pop[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      float v[8];
+      if (full) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          v[r] = s0[c][r];
+          v[4 + r] = s1[c][r];
+        }
       } else {
-        pk[j] = u32x4{0u, 0u, 0u, 0u};
-        pv[j] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i0 = 4 * g + r;
+          const bool ok0 = row_ok[c] & (i0 < rows0) & (k0 + i0 <= q_pos[c]);
+          const bool ok1 = row_ok[c] & (i0 < rows1) & (k0 + 16 + i0 <= q_pos[c]);
+          v[r] = ok0 ? s0[c][r] : -INFINITY;
+          v[4 + r] = ok1 ? s1[c][r] : -INFINITY;
+        }
       }
-    }
-  };
-  auto stash = [&](int buf) {
+      float mx = fmaxf(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])),
+                       fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
+      mx = row_group_max(mx) * a.scale_log2;
+      // The running maximum (exp2 units) moves only when the tile's maximum exceeds it by more
+      // than kRescaleSlack: P then stays <= 2^kRescaleSlack and O is rescaled rarely. Which
+      // maximum is used cancels in O / l; it only sets the scale at which P is rounded.
+      const bool grow = mx > m_run[c] + kRescaleSlack;
+      const float m_next = grow ? mx : m_run[c];
+      const float alpha = grow ? fast_exp2(m_run[c] - m_next) : 1.f;
+      const float m_use = (m_next == -INFINITY) ? 0.f : m_next;
+      float p[8];
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      const int ci = t + 256 * j;
-      const int r = ci / CPR, col = ci % CPR;
-      *reinterpret_cast<u32x4*>(&sk[buf][r * ROW + 8 * col]) = pk[j];
-      *reinterpret_cast<u32x4*>(&sv[buf][r * ROW + 8 * col]) = pv[j];
-      if (col == 0) s_ok[buf][r] = uint8_t((pok >> j) & 1u);
-    }
-  };
-
-  auto compute_sub = [&](int buf, int key0, int sub) {
-    // 16 keys [key0, key0 + 16) held in rows 16*sub.. of the staged tile.
-    const uint16_t* kb = &sk[buf][(16 * sub) * ROW];
-    const uint16_t* vb = &sv[buf][(16 * sub) * ROW];
-    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int r = 0; r < 8; ++r) p[r] = fast_exp2(fmaf(v[r], a.scale_log2, -m_use));
+      l_run[c] = l_run[c] * alpha +
+                 (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+      m_run[c] = m_next;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      const u32x4 kop = *reinterpret_cast<const u32x4*>(kb + n * ROW + 32 * kk + 8 * g);
-      s = mfma16x16x32(kop, qop[kk], s, Tag{});
-    }
-    const uint32_t okw = *reinterpret_cast<const uint32_t*>(&s_ok[buf][16 * sub + 4 * g]);
-    float sv_[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = key0 + 4 * g + r;
-      const bool ok = row_ok && ((okw >> (8 * r)) & 1u) && (key <= q_pos || !a.causal);
-      sv_[r] = ok ? s[r] * a.scale_log2 : -INFINITY;
-    }
-    float mx = fmaxf(fmaxf(sv_[0], sv_[1]), fmaxf(sv_[2], sv_[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = fast_exp2(sv_[r] - m_use);
-    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    m_run = m_new;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
-#pragma unroll
-      for (int i = 0; i < NT; ++i) o[i] *= alpha;
-    }
-    u32x2 pop;
-    pop[0] = pack2(p[0], p[1], Tag{});
-    pop[1] = pack2(p[2], p[3], Tag{});
-    u32x4 vr[4][NC];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        vr[r][c] = *reinterpret_cast<const u32x4*>(vb + (4 * g + r) * ROW + 128 * c + 8 * n);
+        for (int i = 0; i < NT; ++i) o[c][i] *= alpha;
       }
+      pop[c][0] = pack2(p[0], p[1], Tag{});
+      pop[c][1] = pack2(p[2], p[3], Tag{});
+      pop[c][2] = pack2(p[4], p[5], Tag{});
+      pop[c][3] = pack2(p[6], p[7], Tag{});
     }
+    // O^T[16 d x 16 rows] += V^T[16 d x 32 keys] . P^T[32 keys x 16 rows]; k-slots 8g..8g+7 of a
+    // lane are keys 4g..4g+3 of sub-tile 0 then of sub-tile 1, for V and P alike.
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
+    for (int cg = 0; cg < NC; ++cg) {
+      u32x4 vr[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int r0 = 4 * g + r, r1 = 16 + 4 * g + r;
+        vr[r] = *reinterpret_cast<const u32x4*>(sv + r0 * D + (((16 * cg + n) ^ lds_swizzle(r0)) * 8));
+        vr[4 + r] =
+            *reinterpret_cast<const u32x4*>(sv + r1 * D + (((16 * cg + n) ^ lds_swizzle(r1)) * 8));
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        u32x2 vop;
-        vop[0] = __builtin_amdgcn_perm(vr[1][c][e >> 1], vr[0][c][e >> 1], sel);
-        vop[1] = __builtin_amdgcn_perm(vr[3][c][e >> 1], vr[2][c][e >> 1], sel);
-        o[8 * c + e] = mfma16x16x16(vop, pop, o[8 * c + e], Tag{});
+        u32x4 vop;
+        vop[0] = __builtin_amdgcn_perm(vr[1][e >> 1], vr[0][e >> 1], sel);
+        vop[1] = __builtin_amdgcn_perm(vr[3][e >> 1], vr[2][e >> 1], sel);
+        vop[2] = __builtin_amdgcn_perm(vr[5][e >> 1], vr[4][e >> 1], sel);
+        vop[3] = __builtin_amdgcn_perm(vr[7][e >> 1], vr[6][e >> 1], sel);
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          o[c][8 * cg + e] = mfma16x16x32(vop, pop[c], o[c][8 * cg + e], Tag{});
+        }
       }
     }
   };
 
-  if (ntiles > 0) fetch(0);
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
-    stash(buf);
-    __syncthreads();
-    if (it + 1 < ntiles) fetch((it + 1) * kKT);
-    const int k0 = it * kKT;
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      // A sub-tile wholly above this wave's diagonal contributes nothing: skip it (uniform).
-      if (k0 + 16 * sub <= wave_last_key) compute_sub(buf, k0 + 16 * sub, sub);
+  if (ntiles > 0) {
+    load_ids(0);
+    fetch(sk0, sv0, rows_st[0], 0);
+    if (ntiles > 1) load_ids(kKT);
+  }
+  // Two tiles per trip so that each stage is a compile-time array.
+  for (int it = 0; it < ntiles; it += 2) {
+    __syncthreads();  // stage 0 holds tile it; every wave is done with stage 1
+    if (it + 1 < ntiles) {
+      fetch(sk1, sv1, rows_st[1], (it + 1) * kKT);
+      if (it + 2 < ntiles) load_ids((it + 2) * kKT);
     }
+    if (it * kKT <= wave_last_key) compute(sk0, sv0, rows_st[0], it * kKT);
+    if (it + 1 >= ntiles) break;
+    __syncthreads();  // stage 1 holds tile it + 1; every wave is done with stage 0
+    if (it + 2 < ntiles) {
+      fetch(sk0, sv0, rows_st[0], (it + 2) * kKT);
+      if (it + 3 < ntiles) load_ids((it + 3) * kKT);
+    }
+    if ((it + 1) * kKT <= wave_last_key) compute(sk1, sv1, rows_st[1], (it + 1) * kKT);
   }
 
-  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
-  if (!row_ok) return;
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  uint16_t* orow = a.out + int64_t(q_start + q0 + n) * a.o_st + int64_t(h) * a.o_sh;
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
+  for (int c = 0; c < C; ++c) {
+    const float l_tot = row_group_sum(l_run[c]);
+    if (!row_ok[c]) continue;
+    const int rho = wave * 16 * C + 16 * c + n;
+    const int tok = rho / G;
+    const int hh = rho - tok * G;
+    uint16_t* orow =
+        a.out + int64_t(q_start + qb0 + tok) * a.o_st + int64_t(kvh * G + hh) * a.o_sh;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      u32x4 w;
+    for (int cg = 0; cg < NC; ++cg) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        w[k] = pack2(o[8 * c + 2 * k][r] * inv, o[8 * c + 2 * k + 1][r] * inv, Tag{});
+      for (int r = 0; r < 4; ++r) {
+        u32x4 w;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          w[k] = pack2(o[c][8 * cg + 2 * k][r] * inv, o[c][8 * cg + 2 * k + 1][r] * inv, Tag{});
+        }
+        *reinterpret_cast<u32x4*>(orow + 128 * cg + 32 * g + 8 * r) = w;
       }
-      *reinterpret_cast<u32x4*>(orow + 128 * c + 32 * g + 8 * r) = w;
     }
   }
+}
+
+template <int D, int C, int W>
+void launch_prefill(const PrefillArgs& a0, int batch, int max_q, bool bf16, hipStream_t s) {
+  PrefillArgs a = a0;
+  a.tq = (16 * C * W) / a.group;
+  const dim3 grid(unsigned(a.hkv), unsigned(ceil_div(max_q, a.tq)), unsigned(batch));
+  if (bf16) hipLaunchKernelGGL((prefill_mfma_kernel<D, C, W, Bf16>), grid, dim3(64 * W), 0, s, a);
+  else hipLaunchKernelGGL((prefill_mfma_kernel<D, C, W, F16>), grid, dim3(64 * W), 0, s, a);
 }
 
 }  // namespace
@@ -267,6 +393,10 @@ extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q
   if (batch < 0 || total_q < 0 || max_seqlen_q < 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
       num_q_heads % num_kv_heads != 0 || max_blocks_per_seq < 0 || num_blocks < 0) {
     return fail(TI_EINVAL, "ti_gqa_prefill_paged: bad sizes");
+  }
+  if (num_q_heads / num_kv_heads > 64) {
+    return fail(TI_EUNSUPPORTED, "ti_gqa_prefill_paged: %d query heads per KV head (max 64)",
+                num_q_heads / num_kv_heads);
   }
   if (head_dim != 128 && head_dim != 256) {
     return fail(TI_EUNSUPPORTED, "ti_gqa_prefill_paged: head_dim %d not built (128, 256)",
@@ -310,15 +440,9 @@ extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q
   a.max_blocks = max_blocks_per_seq;
   a.causal = causal ? 1 : 0;
   a.scale_log2 = float(1.4426950408889634 / sqrt(double(head_dim)));
-  const dim3 grid(unsigned(ceil_div(max_seqlen_q, kQB)), unsigned(num_q_heads), unsigned(batch));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf16 = dtype == TI_DTYPE_BF16;
-  if (head_dim == 256) {
-    if (bf16) hipLaunchKernelGGL((prefill_mfma_kernel<256, Bf16>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((prefill_mfma_kernel<256, F16>), grid, dim3(256), 0, s, a);
-  } else {
-    if (bf16) hipLaunchKernelGGL((prefill_mfma_kernel<128, Bf16>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((prefill_mfma_kernel<128, F16>), grid, dim3(256), 0, s, a);
-  }
+  if (head_dim == 256) launch_prefill<256, 1, 8>(a, batch, max_seqlen_q, bf16, s);
+  else launch_prefill<128, 2, 8>(a, batch, max_seqlen_q, bf16, s);
   return check_launch("ti_gqa_prefill_paged");
 }
