@@ -66,12 +66,16 @@ int ti_kv_append(const void* key, const void* value, int64_t key_row_stride,
                  int32_t dtype, void* stream);
 
 /*
- * Launch plan of a paged decode call: the split-K partition length actually used, the maximum
- * number of partitions per sequence, and the fp32 workspace the call needs (0 when every sequence
- * fits one partition). `split_tokens` <= 0 asks the library to choose; a positive value is used as
- * given after validation (a multiple of 32 and of page_size). The plan depends only on host-known
- * bounds, so it is valid for any seqlen values <= max_blocks_per_seq * page_size and it is safe to
- * compute once and reuse under graph capture.
+ * Launch plan of a paged decode call and the fp32 workspace it needs.
+ *   split_tokens > 0: fixed split-K -- one workgroup per (sequence, partition of split_tokens);
+ *     outputs the split used, the maximum partitions per sequence, and the workspace (0 when every
+ *     sequence fits one partition). The value must be a multiple of 32 and of page_size.
+ *   split_tokens <= 0: balanced -- one round of workgroups shares the batch's 16-token tiles
+ *     evenly whatever the per-sequence lengths (sequences cut between workgroups are merged in a
+ *     fixed order); outputs split_tokens_out = 0, max_splits_out = the number of workgroups, and a
+ *     workspace that also covers the scalar variant's own plan.
+ * The plan depends only on host-known bounds, so it is valid for any seqlen values <=
+ * max_blocks_per_seq * page_size and it is safe to compute once and reuse under graph capture.
  *
  * No reference counterpart: the reference decode has no split-K (kernels/gqa_decode_paged.py:73,
  * one CTA per (sequence, KV head)); this is the sizing half of the split-K design.

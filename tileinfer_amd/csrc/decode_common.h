@@ -91,7 +91,14 @@ struct DecodeArgs {
   int32_t num_blocks32;  // block ids in [0, num_blocks32) are valid (int32 ids)
   int32_t hq, hkv, group, page_size, max_blocks, max_splits, split_tokens;
   float scale_log2;
+  // Balanced mode (> 0): this many workgroups share the batch's 16-token tiles evenly (every
+  // workgroup takes a contiguous run of the concatenated tiles of all sequences); partials are
+  // indexed [workgroup][first|last segment][q-head]. 0: one workgroup per (sequence, partition of
+  // split_tokens), partials indexed [sequence][q-head][partition].
+  int32_t balanced_wgs;
+  int32_t chunk_min_tiles;  // lower bound on a balanced workgroup's run
 };
+
 
 // Clamped context length of sequence b and its number of partitions.
 __device__ __forceinline__ int seq_len(const DecodeArgs& a, int b) {
@@ -100,6 +107,9 @@ __device__ __forceinline__ int seq_len(const DecodeArgs& a, int b) {
   ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
   return ctx;
 }
+
+// Tiles (16 tokens) of sequence b.
+__device__ __forceinline__ int seq_tiles(const DecodeArgs& a, int b) { return (seq_len(a, b) + 15) >> 4; }
 
 
 // Launches the LDS-staged scalar variant of the partial kernel (gqa_decode_scalar.hip).

@@ -52,14 +52,38 @@ struct Tile {
   int rows;             // tokens of the tile that exist (uniform)
 };
 
+// Wave-wide inclusive prefix sum.
+__device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ int wave_sum(int x) {
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) x += __shfl_xor(x, d, 64);
+  return x;
+}
+
+// Total 16-token tiles of the batch and the balanced run length (same in every workgroup and in
+// the merge: a pure function of the sequence lengths and the plan).
+__device__ __forceinline__ int balanced_chunk(const DecodeArgs& a, int total_tiles) {
+  const int per = (total_tiles + a.balanced_wgs - 1) / a.balanced_wgs;
+  return max(per, a.chunk_min_tiles);
+}
+
 template <int D, typename Tag, int WPB, int POL>
-__global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int batch) {
   constexpr int KK = D / 32;
   constexpr int NC = D / 128;
   constexpr int NT = D / 16;
   static_assert(D % 128 == 0, "head_dim must be a multiple of 128");
 
   __shared__ int s_bids[kMaxSplitPages];
+  __shared__ int s_part[WPB + 4];
 
   const int lane = threadIdx.x & 63;
   // Uniform across the wave; readfirstlane lets the compiler keep it (and every page address
@@ -68,44 +92,18 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
   const int n = lane & 15;  // MFMA row/col index: token row of K, head of S^T/O^T, d-col of V^T
   const int g = lane >> 4;  // MFMA k-group
   const int kvh = blockIdx.x * WPB + wave;
-  const int split = blockIdx.y;
-  const int b = blockIdx.z;
-
-  const int ctx = seq_len(a, b);
-  const int nsplit = (ctx + a.split_tokens - 1) / a.split_tokens;
-  if (split >= (nsplit > 0 ? nsplit : 1)) return;  // uniform over the workgroup
-  const int tok0 = split * a.split_tokens;
-  const int tok1 = min(tok0 + a.split_tokens, ctx);
-  const int page0 = tok0 / a.page_size;
-  const int npages = tok1 > tok0 ? (tok1 - tok0 + a.page_size - 1) / a.page_size : 0;
-  for (int i = threadIdx.x; i < npages; i += 64 * WPB) {
-    s_bids[i] = a.block_table[b * a.bt_stride + page0 + i];
-  }
-  __syncthreads();
-
   const int h = kvh * a.group + n;
   const bool head_ok = n < a.group;
-
-  // Query group as the B operand of S^T = K . Q^T; rows beyond the group stay zero.
-  u32x4 qop[KK];
-  {
-    const uint16_t* qrow = a.q + b * a.q_sb + int64_t(h) * a.q_sh;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      qop[kk] = head_ok ? load16(qrow + 32 * kk + 8 * g) : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
 
   // Byte offsets of this lane's loads inside one 16-token tile of its KV head.
   const uint32_t row_bytes = uint32_t(a.row_stride) * 2;
   const uint32_t lane_k = uint32_t(n) * row_bytes + 16 * g;
   const uint32_t lane_v = uint32_t(4 * g) * row_bytes + 16 * n;
 
+  u32x4 qop[KK];
   f32x4 o[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;
-  float l_run = 0.f;
+  float m_run, l_run, l_tot;
+  int tok0, tok1;
 
   // Loads the 16-token tile at position p into `T`. Every load is issued unconditionally through
   // a buffer descriptor that spans only the tile's rows that exist (in the partition and with a
@@ -114,7 +112,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
   // prefetched behind it.
   auto load_tile = [&](Tile<D>& T, int p) {
     // Past the partition end the LDS entry may be stale; `rows` is 0 there and masks it.
-    const int slot = min((p - tok0) / a.page_size, kMaxSplitPages - 1);
+    const int slot = min(p / a.page_size - tok0 / a.page_size, kMaxSplitPages - 1);
     const int id = __builtin_amdgcn_readfirstlane(s_bids[slot]);
     const bool ok = (tok1 - p > 0) && (uint32_t(id) < uint32_t(a.num_blocks32));
     const int rows = ok ? min(tok1 - p, 16) : 0;
@@ -174,28 +172,51 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
     }
   };
 
-  // Two tiles in flight: the next tile's loads are issued before the current one is consumed.
-  const int ntiles = (tok1 - tok0 + 15) / 16;
-  if (ntiles > 0) {
-    Tile<D> ta, tb;
-    load_tile(ta, tok0);
-    int it = 0;
-    for (; it + 2 <= ntiles; it += 2) {
-      const int t0 = tok0 + 16 * it;
-      load_tile(tb, t0 + 16);
-      compute_tile(ta);
-      if (it + 2 < ntiles) load_tile(ta, t0 + 32);
-      compute_tile(tb);
+  // Attention of this wave's query group over tokens [t0, t1) of sequence b (16-aligned t0):
+  // leaves the unnormalised (o, m_run) and the head's denominator l_tot. Uniform over the
+  // workgroup (it stages the partition's block ids in LDS).
+  auto run_partition = [&](int b, int t0, int t1) {
+    tok0 = t0;
+    tok1 = t1;
+    const int page0 = tok0 / a.page_size;
+    // The plan keeps every partition within kMaxSplitPages pages; the clamp only guards LDS.
+    const int npages = tok1 > tok0 ? min((tok1 - 1) / a.page_size - page0 + 1, kMaxSplitPages) : 0;
+    __syncthreads();  // the previous partition's tiles are done with s_bids
+    for (int i = threadIdx.x; i < npages; i += 64 * WPB) {
+      s_bids[i] = a.block_table[b * a.bt_stride + page0 + i];
     }
-    if (it < ntiles) compute_tile(ta);
-  }
+    __syncthreads();
+    // Query group as the B operand of S^T = K . Q^T; rows beyond the group stay zero.
+    const uint16_t* qrow = a.q + b * a.q_sb + int64_t(h) * a.q_sh;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      qop[kk] = head_ok ? load16(qrow + 32 * kk + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run = -INFINITY;
+    l_run = 0.f;
+    // Two tiles in flight: the next tile's loads are issued before the current one is consumed.
+    const int ntiles = (tok1 - tok0 + 15) / 16;
+    if (ntiles > 0) {
+      Tile<D> ta, tb;
+      load_tile(ta, tok0);
+      int it = 0;
+      for (; it + 2 <= ntiles; it += 2) {
+        const int p0 = tok0 + 16 * it;
+        load_tile(tb, p0 + 16);
+        compute_tile(ta);
+        if (it + 2 < ntiles) load_tile(ta, p0 + 32);
+        compute_tile(tb);
+      }
+      if (it < ntiles) compute_tile(ta);
+    }
+    // Sum the per-lane partial denominators of each head (lanes n, n+16, n+32, n+48).
+    l_tot = l_run + __shfl_xor(l_run, 16, 64);
+    l_tot += __shfl_xor(l_tot, 32, 64);
+  };
 
-  // Sum the per-lane partial denominators of each head (lanes n, n+16, n+32, n+48).
-  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
-  if (!head_ok) return;
-
-  if (nsplit <= 1) {
+  auto store_out = [&](int b) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     uint16_t* orow = a.out + (int64_t(b) * a.hq + h) * D;
 #pragma unroll
@@ -210,8 +231,9 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
         *reinterpret_cast<u32x4*>(orow + 128 * c + 32 * g + 8 * r) = w;
       }
     }
-  } else {
-    const int64_t slot = (int64_t(b) * a.hq + h) * a.max_splits + split;
+  };
+
+  auto store_partial = [&](int64_t slot) {
     float* prow = a.part_o + slot * D;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -228,40 +250,180 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a) {
       a.part_ml[2 * slot] = m_run;
       a.part_ml[2 * slot + 1] = l_tot;
     }
+  };
+
+  if (a.balanced_wgs == 0) {
+    // One workgroup per (sequence, partition of split_tokens).
+    const int split = blockIdx.y;
+    const int b = blockIdx.z;
+    const int ctx = seq_len(a, b);
+    const int nsplit = (ctx + a.split_tokens - 1) / a.split_tokens;
+    if (split >= (nsplit > 0 ? nsplit : 1)) return;  // uniform over the workgroup
+    const int t0 = split * a.split_tokens;
+    run_partition(b, t0, min(t0 + a.split_tokens, ctx));
+    if (!head_ok) return;
+    if (nsplit <= 1) store_out(b);
+    else store_partial((int64_t(b) * a.hq + h) * a.max_splits + split);
+    return;
+  }
+
+  // Balanced: workgroup i takes tiles [i * chunk, (i + 1) * chunk) of the batch's concatenated
+  // 16-token tiles. Wave 0 finds the first and last sequence of that run with a prefix scan.
+  const int i = blockIdx.y;
+  if (wave == 0) {
+    int tot = 0;
+    for (int b0 = 0; b0 < batch; b0 += 64) {
+      tot += wave_sum(b0 + lane < batch ? seq_tiles(a, b0 + lane) : 0);
+    }
+    const int chunk = balanced_chunk(a, tot);
+    const int T0 = i * chunk;
+    const int T1 = min(T0 + chunk, tot);
+    int carry = 0, b_first = -1, s_first = 0, b_last = -1;
+    if (T0 < T1) {
+      for (int b0 = 0; b0 < batch && carry < T1; b0 += 64) {
+        const int nt = b0 + lane < batch ? seq_tiles(a, b0 + lane) : 0;
+        const int incl = wave_inclusive_scan(nt, lane) + carry;
+        const int excl = incl - nt;
+        const bool has_first = nt > 0 && excl <= T0 && T0 < incl;
+        const bool has_last = nt > 0 && excl <= T1 - 1 && T1 - 1 < incl;
+        const uint64_t mf = __builtin_amdgcn_ballot_w64(has_first);
+        const uint64_t ml = __builtin_amdgcn_ballot_w64(has_last);
+        if (mf) {
+          const int src = __builtin_ctzll(mf);
+          b_first = b0 + src;
+          s_first = __shfl(excl, src, 64);
+        }
+        if (ml) b_last = b0 + __builtin_ctzll(ml);
+        carry = __shfl(incl, 63, 64);
+      }
+    }
+    if (lane == 0) {
+      s_part[0] = T0;
+      s_part[1] = T1;
+      s_part[2] = b_first;
+      s_part[3] = s_first;
+      s_part[4] = b_last;
+    }
+  }
+  __syncthreads();
+  const int T0 = __builtin_amdgcn_readfirstlane(s_part[0]);
+  const int T1 = __builtin_amdgcn_readfirstlane(s_part[1]);
+  const int b_first = __builtin_amdgcn_readfirstlane(s_part[2]);
+  const int b_last = __builtin_amdgcn_readfirstlane(s_part[4]);
+  if (T0 >= T1 || b_first < 0 || b_last < b_first) return;  // uniform: no work
+  int sb = __builtin_amdgcn_readfirstlane(s_part[3]);
+  for (int b = b_first; b <= b_last; ++b) {
+    const int nb = __builtin_amdgcn_readfirstlane(seq_tiles(a, b));
+    if (nb > 0) {
+      const int t0 = max(T0, sb) - sb;
+      const int t1 = min(T1, sb + nb) - sb;
+      const int ctx = __builtin_amdgcn_readfirstlane(seq_len(a, b));
+      run_partition(b, 16 * t0, min(16 * t1, ctx));
+      if (head_ok) {
+        if (t0 == 0 && t1 == nb) store_out(b);
+        else store_partial((int64_t(i) * 2 + (b == b_first ? 0 : 1)) * a.hq + h);
+      }
+    }
+    sb += nb;
   }
 }
 
-// Combines the partition partials of every (sequence, q-head) whose sequence spans more than
-// one partition, in partition order (deterministic): m = max m_s, w_s = 2^(m_s - m),
-// out = sum w_s o_s / sum w_s l_s.
+// Combines the partials of every (sequence, q-head) whose context was split over more than one
+// workgroup, in workgroup order (deterministic): m = max m_s, w_s = 2^(m_s - m),
+// out = sum w_s o_s / sum w_s l_s. In balanced mode it also writes the zero rows of empty
+// sequences (no workgroup covers them).
 template <int D, typename Tag>
-__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batch) {
   constexpr int PER = D / 64;  // d-values per thread
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int ctx = seq_len(a, b);
-  const int nsplit = (ctx + a.split_tokens - 1) / a.split_tokens;
-  if (nsplit <= 1) return;
-  const int64_t slot0 = (int64_t(b) * a.hq + h) * a.max_splits;
+  const int lane = threadIdx.x;
+  const int d0 = lane * PER;
+  uint16_t* orow = a.out + (int64_t(b) * a.hq + h) * D + d0;
+  int64_t slot0 = 0, stride = 1;
+  int nparts = 0;
+  int first_part_slot1 = 0;  // balanced: the first part sits in slot 1 of its workgroup
+  if (a.balanced_wgs == 0) {
+    const int ctx = seq_len(a, b);
+    nparts = (ctx + a.split_tokens - 1) / a.split_tokens;
+    if (nparts <= 1) return;
+    slot0 = (int64_t(b) * a.hq + h) * a.max_splits;
+  } else {
+    const int nb = seq_tiles(a, b);
+    if (nb == 0) {
+#pragma unroll
+      for (int j = 0; j < PER; j += 2) *reinterpret_cast<uint32_t*>(orow + j) = 0u;
+      return;
+    }
+    int tot = 0, pre = 0;
+    for (int b0 = 0; b0 < batch; b0 += 64) {
+      const int j = b0 + lane;
+      const int nt = j < batch ? seq_tiles(a, j) : 0;
+      tot += nt;
+      pre += j < b ? nt : 0;
+    }
+    tot = wave_sum(tot);
+    pre = wave_sum(pre);
+    const int chunk = balanced_chunk(a, tot);
+    const int i0 = pre / chunk;
+    const int i1 = (pre + nb - 1) / chunk;
+    if (i0 == i1) return;  // one workgroup covered the whole sequence and wrote it
+    nparts = i1 - i0 + 1;
+    first_part_slot1 = (i0 * chunk < pre) ? 1 : 0;
+    slot0 = int64_t(i0) * 2 * a.hq + h;
+    stride = 2 * a.hq;
+  }
+  // Part s lives at slot0 + s * stride (+ hq for a first part stored as its workgroup's last).
+  auto part = [&](int s) -> int64_t {
+    return slot0 + s * stride + ((s == 0 && first_part_slot1) ? a.hq : 0);
+  };
+  // Maximum over the parts' m, lane-parallel.
   float m = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) m = fmaxf(m, a.part_ml[2 * (slot0 + s)]);
+  for (int s0 = 0; s0 < nparts; s0 += 64) {
+    const int s = s0 + lane;
+    m = fmaxf(m, s < nparts ? a.part_ml[2 * part(s)] : -INFINITY);
+  }
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
   float acc[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) acc[j] = 0.f;
   float l = 0.f;
-  const int d0 = threadIdx.x * PER;
   if (m != -INFINITY) {
-    for (int s = 0; s < nsplit; ++s) {
-      const float ms = a.part_ml[2 * (slot0 + s)];
-      const float w = ms == -INFINITY ? 0.f : fast_exp2(ms - m);
-      l += w * a.part_ml[2 * (slot0 + s) + 1];
-      const float* src = a.part_o + (slot0 + s) * D + d0;
+    // Parts in chunks of 64: lane s holds part s0+s's weight; the o rows of 8 parts are loaded
+    // back to back so their latencies overlap. Summation order is fixed (ascending part).
+    for (int s0 = 0; s0 < nparts; s0 += 64) {
+      const int s = s0 + lane;
+      float w = 0.f, wl = 0.f;
+      if (s < nparts) {
+        const int64_t ps = part(s);
+        const float ms = a.part_ml[2 * ps];
+        w = ms == -INFINITY ? 0.f : fast_exp2(ms - m);
+        wl = w * a.part_ml[2 * ps + 1];
+      }
+      const int cnt = min(64, nparts - s0);
+      for (int j0 = 0; j0 < cnt; j0 += 8) {
+        float v[8][PER];
+        float wj[8];
 #pragma unroll
-      for (int j = 0; j < PER; ++j) acc[j] += w * src[j];
+        for (int u = 0; u < 8; ++u) {
+          wj[u] = __shfl(w, j0 + u, 64);
+          const bool live = j0 + u < cnt;
+          const float* src = a.part_o + part(s0 + (live ? j0 + u : 0)) * D + d0;
+#pragma unroll
+          for (int q = 0; q < PER; ++q) v[u][q] = live ? src[q] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+#pragma unroll
+          for (int q = 0; q < PER; ++q) acc[q] += wj[u] * v[u][q];
+        }
+      }
+      // l in the same ascending order on every lane.
+      for (int j = 0; j < cnt; ++j) l += __shfl(wl, j, 64);
     }
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  uint16_t* orow = a.out + (int64_t(b) * a.hq + h) * D + d0;
 #pragma unroll
   for (int j = 0; j < PER; j += 2) {
     *reinterpret_cast<uint32_t*>(orow + j) = pack2(acc[j] * inv, acc[j + 1] * inv, Tag{});
@@ -270,13 +432,14 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
 
 template <int D, typename Tag, int WPB>
 int launch_mfma(const DecodeArgs& a, int batch, bool reuse_kv, hipStream_t stream) {
-  const dim3 grid(a.hkv / WPB, a.max_splits, batch);
+  const dim3 grid = a.balanced_wgs > 0 ? dim3(a.hkv / WPB, a.balanced_wgs, 1)
+                                        : dim3(a.hkv / WPB, a.max_splits, batch);
   if (reuse_kv) {
     hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyKeep>), grid, dim3(64 * WPB), 0,
-                       stream, a);
+                       stream, a, batch);
   } else {
     hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyStream>), grid, dim3(64 * WPB), 0,
-                       stream, a);
+                       stream, a, batch);
   }
   return check_launch("ti_gqa_decode_paged (mfma)");
 }
@@ -292,8 +455,9 @@ int launch_decode(const DecodeArgs& a, int batch, bool reuse_kv, hipStream_t str
     rc = launch_mfma<D, Tag, 1>(a, batch, reuse_kv, stream);
   }
   if (rc != TI_OK) return rc;
-  if (a.max_splits > 1) {
-    hipLaunchKernelGGL((decode_merge_kernel<D, Tag>), dim3(a.hq, batch), dim3(64), 0, stream, a);
+  if (a.balanced_wgs > 0 || a.max_splits > 1) {
+    hipLaunchKernelGGL((decode_merge_kernel<D, Tag>), dim3(a.hq, batch), dim3(64), 0, stream, a,
+                       batch);
     return check_launch("ti_gqa_decode_paged (merge)");
   }
   return TI_OK;
@@ -309,8 +473,19 @@ int64_t lcm64(int64_t x, int64_t y) {
   return x / p * y;
 }
 
+// Launch plans of one decode call. `split`/`max_splits`/`ws_fixed`: one workgroup per
+// (sequence, partition of `split` tokens) -- the requested split, or the heuristic one for the
+// scalar variant. `balanced_wgs`/`ws_balanced`: the MFMA variant's balanced mode when no split was
+// requested (0 otherwise).
+struct Plan {
+  int32_t split = 0, max_splits = 1, balanced_wgs = 0, chunk_min_tiles = 0;
+  int64_t ws_fixed = 0, ws_balanced = 0;
+};
+
+constexpr int kMinChunkTiles = 4;  // 64 tokens: shorter runs are dominated by start-up
+
 int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, int32_t max_blocks,
-         int32_t split_req, int32_t* split_out, int32_t* max_splits_out, int64_t* ws_out) {
+         int32_t split_req, Plan* out) {
   if (batch < 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0) {
     return fail(TI_EINVAL, "decode: bad head counts batch=%d hq=%d hkv=%d", batch, hq, hkv);
   }
@@ -330,6 +505,7 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
     return fail(TI_EINVAL, "decode: context bound %lld too large", (long long)bound);
   }
   const int64_t unit = lcm64(32, page_size);
+  const int64_t cus = device_cu_count();
   int64_t split;
   if (split_req > 0) {
     split = split_req;
@@ -342,7 +518,6 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
     // Fewest, longest partitions that still give every CU a workgroup: each workgroup pays a
     // start-up (block ids, first tile) and drain that nothing else on its CU hides, so on MI355X
     // one full round of long workgroups streams fastest (config 3: 8,192 tokens, 256 workgroups).
-    const int64_t cus = device_cu_count();
     const int64_t wpb = (hkv % 4 == 0) ? 4 : (hkv % 2 == 0) ? 2 : 1;  // waves per workgroup
     const int64_t wgs_per_split = int64_t(batch) * (hkv / wpb);
     split = kMaxSplitTokens;
@@ -353,9 +528,27 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
   }
   int64_t max_splits = bound > 0 ? ceil_div(bound, split) : 1;
   if (max_splits > 65535) return fail(TI_EINVAL, "decode: %lld partitions", (long long)max_splits);
-  *split_out = int32_t(split);
-  *max_splits_out = int32_t(max_splits);
-  *ws_out = max_splits > 1 ? int64_t(batch) * hq * max_splits * (D + 2) * 4 : 0;
+  out->split = int32_t(split);
+  out->max_splits = int32_t(max_splits);
+  out->ws_fixed = max_splits > 1 ? int64_t(batch) * hq * max_splits * (D + 2) * 4 : 0;
+  out->balanced_wgs = 0;
+  out->ws_balanced = 0;
+  if (split_req <= 0) {
+    // Balanced mode: one round of workgroups over the batch's tiles; enough workgroups that no
+    // run exceeds the block ids one workgroup stages in LDS (a run may start mid-page: one page
+    // of slack).
+    const int64_t max_chunk = int64_t(kMaxSplitPages - 1) * (page_size / 16);
+    const int64_t bound_tiles = ceil_div(bound, 16);
+    const int64_t wpb = (hkv % 4 == 0) ? 4 : (hkv % 2 == 0) ? 2 : 1;
+    const int64_t per_round = cus / (hkv / wpb) > 0 ? cus / (hkv / wpb) : 1;
+    int64_t wgs = per_round;
+    wgs = wgs > ceil_div(int64_t(batch) * bound_tiles, max_chunk)
+              ? wgs : ceil_div(int64_t(batch) * bound_tiles, max_chunk);
+    if (wgs > 65535) return fail(TI_EINVAL, "decode: %lld balanced workgroups", (long long)wgs);
+    out->balanced_wgs = int32_t(wgs);
+    out->chunk_min_tiles = int32_t(kMinChunkTiles < max_chunk ? kMinChunkTiles : max_chunk);
+    out->ws_balanced = wgs * 2 * hq * (D + 2) * 4;
+  }
   return TI_OK;
 }
 
@@ -369,8 +562,21 @@ extern "C" int ti_gqa_decode_plan(int32_t batch, int32_t num_q_heads, int32_t nu
   if (!split_tokens_out || !max_splits_out || !workspace_bytes_out) {
     return ti::fail(TI_EINVAL, "ti_gqa_decode_plan: null output pointer");
   }
-  return ti::plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq,
-                  split_tokens, split_tokens_out, max_splits_out, workspace_bytes_out);
+  ti::Plan p;
+  const int rc = ti::plan(batch, num_q_heads, num_kv_heads, head_dim, page_size,
+                          max_blocks_per_seq, split_tokens, &p);
+  if (rc != TI_OK) return rc;
+  if (split_tokens > 0) {
+    *split_tokens_out = p.split;
+    *max_splits_out = p.max_splits;
+    *workspace_bytes_out = p.ws_fixed;
+  } else {
+    // Balanced (MFMA) plan; the workspace also covers the scalar variant's fixed plan.
+    *split_tokens_out = 0;
+    *max_splits_out = p.balanced_wgs;
+    *workspace_bytes_out = p.ws_balanced > p.ws_fixed ? p.ws_balanced : p.ws_fixed;
+  }
+  return TI_OK;
 }
 
 extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -392,11 +598,13 @@ extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_
       (variant & ~(0xF | TI_DECODE_REUSE_KV)) != 0) {
     return fail(TI_EINVAL, "ti_gqa_decode_paged: unknown variant/flags 0x%x", variant);
   }
-  int32_t split = 0, max_splits = 0;
-  int64_t ws_need = 0;
+  Plan pl;
   int rc = plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq,
-                split_tokens, &split, &max_splits, &ws_need);
+                split_tokens, &pl);
   if (rc != TI_OK) return rc;
+  const bool balanced = kind != TI_DECODE_SCALAR && pl.balanced_wgs > 0;
+  const int32_t split = pl.split, max_splits = pl.max_splits;
+  const int64_t ws_need = balanced ? pl.ws_balanced : pl.ws_fixed;
   if (batch == 0) return TI_OK;
   if (!q || !k_cache || !v_cache || !block_table || !seqlen || !out) {
     return fail(TI_EINVAL, "ti_gqa_decode_paged: null pointer");
@@ -428,7 +636,11 @@ extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_
   a.seqlen = seqlen;
   a.out = static_cast<uint16_t*>(out);
   a.part_o = static_cast<float*>(workspace);
-  a.part_ml = a.part_o ? a.part_o + int64_t(batch) * num_q_heads * max_splits * head_dim : nullptr;
+  const int64_t n_parts =
+      balanced ? int64_t(pl.balanced_wgs) * 2 * num_q_heads : int64_t(batch) * num_q_heads * max_splits;
+  a.part_ml = a.part_o ? a.part_o + n_parts * head_dim : nullptr;
+  a.balanced_wgs = balanced ? pl.balanced_wgs : 0;
+  a.chunk_min_tiles = pl.chunk_min_tiles;
   a.num_blocks32 = int32_t(num_blocks < INT32_MAX ? num_blocks : INT32_MAX);
   a.hq = num_q_heads;
   a.hkv = num_kv_heads;
@@ -445,11 +657,11 @@ extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_
     if (rc != TI_OK) return rc;
     if (max_splits > 1) {
       if (head_dim == 256) {
-        if (bf16) hipLaunchKernelGGL((decode_merge_kernel<256, Bf16>), dim3(num_q_heads, batch), dim3(64), 0, s, a);
-        else hipLaunchKernelGGL((decode_merge_kernel<256, F16>), dim3(num_q_heads, batch), dim3(64), 0, s, a);
+        if (bf16) hipLaunchKernelGGL((decode_merge_kernel<256, Bf16>), dim3(num_q_heads, batch), dim3(64), 0, s, a, batch);
+        else hipLaunchKernelGGL((decode_merge_kernel<256, F16>), dim3(num_q_heads, batch), dim3(64), 0, s, a, batch);
       } else {
-        if (bf16) hipLaunchKernelGGL((decode_merge_kernel<128, Bf16>), dim3(num_q_heads, batch), dim3(64), 0, s, a);
-        else hipLaunchKernelGGL((decode_merge_kernel<128, F16>), dim3(num_q_heads, batch), dim3(64), 0, s, a);
+        if (bf16) hipLaunchKernelGGL((decode_merge_kernel<128, Bf16>), dim3(num_q_heads, batch), dim3(64), 0, s, a, batch);
+        else hipLaunchKernelGGL((decode_merge_kernel<128, F16>), dim3(num_q_heads, batch), dim3(64), 0, s, a, batch);
       }
       return check_launch("ti_gqa_decode_paged (merge)");
     }
