@@ -320,8 +320,11 @@ def run_config(cfg: int, args, dev) -> dict:
     return {
         "metric": METRIC, "config": {"workload": f"config{cfg}", "batch": len(ctx),
                                      "ctx_min": min(ctx), "ctx_max": max(ctx), "ctx_sum": sum(ctx),
-                                     "append_tokens": slots.numel(), "split_tokens": split,
-                                     "max_splits": max_splits, "variant": args.variant},
+                                     "append_tokens": slots.numel(),
+                                     "partition": (f"balanced over {max_splits} workgroups"
+                                                   if split == 0 else
+                                                   f"fixed {split} tokens, up to {max_splits} per sequence"),
+                                     "variant": args.variant},
         "decode_us": round(d_us, 2), "decode_GBps_algorithmic": round(d_bytes / (d_us * 1e-6) / 1e9, 1),
         "decode_pct_of_peak_hbm": round(100 * d_bytes / (d_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 2),
         "append_us": round(a_us, 2), "append_GBps_algorithmic": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
@@ -435,8 +438,10 @@ def main():
             "workload": (f"config3: decode step of {layers} full-attention layers, batch {b} x "
                          f"context {ctx}, 24Q/4KV heads, head_dim 256, block 16, bf16; per layer "
                          f"append {b} tokens then split-K paged decode"),
-            "batch": b, "ctx": ctx, "layers": layers, "split_tokens": split,
-            "max_splits": max_splits, "variant": args.variant,
+            "batch": b, "ctx": ctx, "layers": layers,
+            "partition": (f"balanced over {max_splits} workgroups" if split == 0
+                          else f"fixed {split} tokens, up to {max_splits} per sequence"),
+            "variant": args.variant,
             "tables": "sequential" if args.sequential_tables else "random permutation per layer",
         },
         "us_per_layer_step": round(ms_step * 1e3 / layers, 2),
