@@ -218,6 +218,56 @@ def swap_config5(st, dev, args, layers: int = 16, fraction: float = 0.25) -> dic
             "roundtrip_bit_exact": ok, "bound": "host link (pinned host memory over the fabric)"}
 
 
+def metadata_compare(b: int, ctx: int, dev, steps: int = 16, warmup: int = 2) -> dict:
+    """Per-step decode metadata at the bench's batch and context. The reference runner's host
+    builder (restated in oracle/ref_metadata.py: every sequence's whole block table through
+    torch.tensor into pinned buffers, then the uploads; engine/model_runner.py:538-584) against
+    DeviceBlockTables (the appended ids go up, the GPU derives tables, slots and lengths). Both
+    are timed wall-clock per step including the device work (synchronised)."""
+    from oracle.ref_metadata import RefDecodePrep
+    from tileinfer_amd.engine import DeviceBlockTables, PagedKVManager, Sequence
+
+    width = ctx // BLOCK + 2
+    m = PagedKVManager(b * width, BLOCK, enable_prefix_caching=False)
+    seqs = []
+    for _ in range(b):
+        s = Sequence(range(ctx - 1))
+        if not m.admit(s):
+            raise RuntimeError("metadata_compare: pool too small")
+        m.finish_chunk(s, s.num_tokens)
+        seqs.append(s)
+    ref = RefDecodePrep(b, width, device=dev)
+    dt = DeviceBlockTables(max_seqs=b, max_blocks_per_seq=width, block_size=BLOCK, device=dev)
+    ref_t, dev_t, words = [], [], []
+    for it in range(warmup + steps):
+        for s in seqs:
+            s.append_token(0)
+            m.append_slot(s)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ref(seqs, BLOCK, bsz=b)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        dt.step(seqs, width=width)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        if it >= warmup:
+            ref_t.append((t1 - t0) * 1e6)
+            dev_t.append((t2 - t1) * 1e6)
+            words.append(dt.last_upload_words)
+    rs, rt, rc = ref(seqs, BLOCK, bsz=b)
+    ds, dtb, dc = dt.step(seqs, width=width)
+    same = bool(torch.equal(rs, ds) and torch.equal(rt, dtb) and torch.equal(rc, dc))
+    return {"batch": b, "blocks_per_seq": ctx // BLOCK, "steps": steps,
+            "reference_host_builder_us_per_step": round(statistics.median(ref_t), 1),
+            "device_tables_us_per_step": round(statistics.median(dev_t), 1),
+            "reference_upload_bytes_per_step": 4 * b * (width + 3),
+            "device_upload_bytes_per_step": 4 * int(statistics.median(words)),
+            "outputs_identical": same,
+            "note": "wall clock per step incl. device work; the reference builder is restated "
+                    "in oracle/ref_metadata.py"}
+
+
 def prefill_config4(st, chunk_slots, kc, vc, dev, args) -> dict:
     """Config 4's 2048-token chunk through the paged prefill attention, straight from the cache
     pages the append just wrote (first chunk: the chunk attends over itself), and a continuation
@@ -349,6 +399,8 @@ def main():
     ap.add_argument("--seed", type=int, default=1003)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--no-metadata", action="store_true",
+                    help="skip the per-step metadata comparison (host builder vs device tables)")
     ap.add_argument("--sequential-tables", action="store_true",
                     help="diagnostic: contiguous blocks per sequence instead of random permutations")
     args = ap.parse_args()
@@ -462,6 +514,9 @@ def main():
             "algorithmic_bytes_per_launch": d_bytes,
         },
     }
+    if not args.no_metadata:
+        log("per-step metadata: reference host builder vs device-resident tables")
+        result["metadata"] = metadata_compare(b, ctx, dev)
     if not args.no_parity:
         log("full-size parity sample")
         result["parity"] = parity_sample(kv, tables, seqlen, q, k_new, v_new, out, layers - 1)

@@ -8,6 +8,8 @@
  *   - block copies between caches           (swap out/in and copy-on-write; no reference kernel)
  *   - paged causal GQA prefill attention    (replaces the gather + varlen flash attention of
  *                                            model/qwen_36.py:1030-1065, kernels/gqa_varlen.py)
+ *   - device-resident step metadata         (replaces the runner's per-step table / slot builders,
+ *                                            engine/model_runner.py:538-637)
  *
  * Conventions shared by every entry point
  *   - All tensor pointers are DEVICE pointers owned by the caller. The library never allocates,
@@ -164,6 +166,35 @@ int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                          int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
                          int32_t head_dim, int32_t page_size, int64_t num_blocks,
                          int32_t max_blocks_per_seq, int32_t causal, int32_t dtype, void* stream);
+
+/*
+ * Device-resident paged metadata for one step: persistent block tables updated in place, and the
+ * step's slot mapping, context lengths and -1-padded batch block tables derived on the GPU.
+ *
+ * Replaces the per-step host builders engine/model_runner.py:538-584 (_prepare_decode_into_graph,
+ * including graph padding 580-584), 586-593 (_build_block_tables) and 595-637 (slot mappings),
+ * which rebuild and upload every sequence's whole table each step. Inputs (int32, device):
+ *   tables       [num_rows, table_stride] persistent tables (row = a sequence's slot), updated
+ *   batch_rows   [n] persistent row of batch entry i (distinct within a call)
+ *   ctx_new      [n] context length of entry i after this step's tokens
+ *   table_len    [n] length of entry i's block table (ids copied to bt_out; -1 past them)
+ *   tok_off      [n+1] entry i's new tokens are slot_out[tok_off[i] .. tok_off[i+1]), the last
+ *                tok_off[i+1]-tok_off[i] positions before ctx_new[i] (decode: one token each)
+ *   upd_off      [n+1] entry i's table updates are upd_col/upd_id[upd_off[i] .. upd_off[i+1]):
+ *                tables[batch_rows[i]][upd_col[k]] = upd_id[k] (the ids appended since the last
+ *                step; a whole table for a sequence new to its row)
+ * Outputs: slot_out [tok_off[n] + pad_to - n] (a position without a block gives -1),
+ *   ctx_out [pad_to], bt_out [pad_to, width] at bt_stride (optional, NULL to skip; entries past
+ *   table_len are -1). Entries [n, pad_to) are graph padding: slot -1, context length
+ *   1, block -1 (engine/model_runner.py:524-527). One launch on `stream`.
+ */
+int ti_paged_metadata(int32_t* tables, int64_t table_stride, int32_t num_rows, int32_t max_blocks,
+                      const int32_t* batch_rows, const int32_t* ctx_new,
+                      const int32_t* table_len, const int32_t* tok_off,
+                      const int32_t* upd_off, const int32_t* upd_col, const int32_t* upd_id,
+                      int32_t n, int32_t pad_to, int32_t* slot_out, int32_t* ctx_out,
+                      int32_t* bt_out, int64_t bt_stride, int32_t width, int32_t page_size,
+                      void* stream);
 
 /* Text of the last error reported on the calling thread ("" when none). */
 const char* ti_last_error(void);

@@ -45,6 +45,9 @@ SIGNATURES = {
                                             _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i32, _c_i32,
                                             _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32,
                                             _c_i32, _c_i32, _c_vp]),
+    "ti_paged_metadata": (ctypes.c_int, [_c_vp, _c_i64, _c_i32, _c_i32, _c_vp, _c_vp, _c_vp,
+                                         _c_vp, _c_vp, _c_vp, _c_vp, _c_i32, _c_i32, _c_vp, _c_vp,
+                                         _c_vp, _c_i64, _c_i32, _c_i32, _c_vp]),
     "ti_last_error": (ctypes.c_char_p, []),
     "ti_abi_version": (ctypes.c_int32, []),
 }
