@@ -268,6 +268,79 @@ def metadata_compare(b: int, ctx: int, dev, steps: int = 16, warmup: int = 2) ->
                     "in oracle/ref_metadata.py"}
 
 
+def _graph_us(fn, reps: int = 20, replays: int = 5) -> float:
+    """Mean GPU µs of fn(): `reps` calls captured in one HIP graph, replayed `replays` times and
+    timed with events (no Python launch overhead in the figure)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * replays)
+
+
+def fusions_compare(kv, tables, slots, seqlen, q, dev) -> dict:
+    """One layer of the decode step with the element-wise work around attention (model/qwen_36.py:
+    977-1018 before, 1083 after), unfused against fused, GPU time from captured graphs."""
+    from tileinfer_amd.kernels import (fused_sigmoid_mul, qknorm_rope, qknorm_rope_append,
+                                       store_kvcache as store)
+
+    b = q.shape[1]
+    gen = torch.Generator(device=dev).manual_seed(21)
+    rnd = lambda *sh: torch.randn(sh, generator=gen, device=dev).to(torch.bfloat16)  # noqa: E731
+    q0, k0, v0 = rnd(b, HQ, HEAD_DIM), rnd(b, HKV, HEAD_DIM), rnd(b, HKV, HEAD_DIM)
+    qw, kw = 0.1 * rnd(HEAD_DIM), 0.1 * rnd(HEAD_DIM)
+    pos = torch.arange(b, device=dev, dtype=torch.float32) * 1000.0
+    inv = 1.0 / 1e7 ** (torch.arange(0, 64, 2, device=dev).float() / 64)
+    emb = torch.cat([pos[:, None] * inv, pos[:, None] * inv], dim=-1)
+    cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+    k_rows, v_rows, k_paged, v_paged = layer_views(kv, 0)
+    gate = rnd(b, 1, HQ * HEAD_DIM)
+
+    def unfused_in():
+        qn = qknorm_rope(q0, qw, cos, sin)
+        kn = qknorm_rope(k0, kw, cos, sin)
+        store(kn, v0, k_rows, v_rows, slots[0])
+        return qn
+
+    def fused_in():
+        return qknorm_rope_append(q0, k0, v0, qw, kw, cos, sin, k_rows, v_rows, slots[0])
+
+    def unfused_out():
+        o = gqa_decode_paged_fn(q[0], k_paged, v_paged, tables[0], seqlen, BLOCK)
+        return fused_sigmoid_mul(o, gate)
+
+    def fused_out():
+        return gqa_decode_paged_fn(q[0], k_paged, v_paged, tables[0], seqlen, BLOCK, gate=gate)
+
+    res = {"batch": b,
+           "input_side_unfused_us": round(_graph_us(unfused_in), 2),
+           "input_side_fused_us": round(_graph_us(fused_in), 2),
+           "decode_then_gate_us": round(_graph_us(unfused_out, reps=3, replays=3), 2),
+           "decode_gated_us": round(_graph_us(fused_out, reps=3, replays=3), 2)}
+    same_in = bool(torch.equal(unfused_in().view(torch.int16), fused_in().view(torch.int16)))
+    same_out = bool(torch.equal(unfused_out().view(torch.int16), fused_out().view(torch.int16)))
+    res["bitwise_equal"] = same_in and same_out
+    res["note"] = ("input side: qknorm_rope(q), qknorm_rope(k), store_kvcache vs one "
+                   "qknorm_rope_append; output side: decode + fused_sigmoid_mul vs decode with "
+                   "the gate in its epilogue; per layer, GPU time of captured graphs")
+    return res
+
+
 def prefill_config4(st, chunk_slots, kc, vc, dev, args) -> dict:
     """Config 4's 2048-token chunk through the paged prefill attention, straight from the cache
     pages the append just wrote (first chunk: the chunk attends over itself), and a continuation
@@ -399,6 +472,8 @@ def main():
     ap.add_argument("--seed", type=int, default=1003)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--no-fusions", action="store_true",
+                    help="skip the unfused-vs-fused timing of the element-wise work around attention")
     ap.add_argument("--no-metadata", action="store_true",
                     help="skip the per-step metadata comparison (host builder vs device tables)")
     ap.add_argument("--sequential-tables", action="store_true",
@@ -514,6 +589,9 @@ def main():
             "algorithmic_bytes_per_launch": d_bytes,
         },
     }
+    if not args.no_fusions:
+        log("fusions around attention: unfused vs fused (captured graphs)")
+        result["fusions"] = fusions_compare(kv, tables, slots, seqlen, q, dev)
     if not args.no_metadata:
         log("per-step metadata: reference host builder vs device-resident tables")
         result["metadata"] = metadata_compare(b, ctx, dev)

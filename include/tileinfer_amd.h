@@ -10,6 +10,8 @@
  *                                            model/qwen_36.py:1030-1065, kernels/gqa_varlen.py)
  *   - device-resident step metadata         (replaces the runner's per-step table / slot builders,
  *                                            engine/model_runner.py:538-637)
+ *   - QK-norm + RoPE (+ append), sigmoid     (replace kernels/qknorm_rope.py, kernels/act_mul.py's
+ *     gate (+ in decode's epilogue)          fused_sigmoid_mul around the path)
  *
  * Conventions shared by every entry point
  *   - All tensor pointers are DEVICE pointers owned by the caller. The library never allocates,
@@ -195,6 +197,70 @@ int ti_paged_metadata(int32_t* tables, int64_t table_stride, int32_t num_rows, i
                       int32_t n, int32_t pad_to, int32_t* slot_out, int32_t* ctx_out,
                       int32_t* bt_out, int64_t bt_stride, int32_t width, int32_t page_size,
                       void* stream);
+
+/*
+ * Per-head RMSNorm with a (1 + weight) scale, then rotary embedding of the first rotary_dim
+ * dimensions (rotate-half pairing i <-> i + rotary_dim/2, cos/sin[0 .. rotary_dim/2) for both
+ * halves), for n_tokens x n_heads rows of head_dim values:
+ *   y = x * rsqrt(mean(x^2) + eps) * (1 + weight)   (fp32, rounded to the storage type)
+ *   out[i] = y[i] c_i - y[i+h] s_i,  out[i+h] = y[i+h] c_i + y[i] s_i  (i < h = rotary_dim/2),
+ *   out[i] = y[i] for i >= rotary_dim.
+ * Replaces fused_qknorm_rope(x, weight, cos_flat, sin_flat, eps) (kernels/qknorm_rope.py:52-56,
+ * kernel 9-50) and generalises it to many tokens with per-token cos/sin (row stride cs_stride_t;
+ * 0 = one vector for all tokens, as the reference kernel takes). head_dim 128 or 256; rows 4-byte
+ * aligned; x and out may alias.
+ */
+int ti_qknorm_rope(const void* x, int64_t x_stride_t, int64_t x_stride_h, void* out,
+                   int64_t out_stride_t, int64_t out_stride_h, const void* weight,
+                   const void* cos, const void* sin, int64_t cs_stride_t, int32_t n_tokens,
+                   int32_t n_heads, int32_t head_dim, int32_t rotary_dim, float eps,
+                   int32_t dtype, void* stream);
+
+/*
+ * One launch for the attention inputs of a step (model/qwen_36.py:977-1018): q heads normalised
+ * and rotated into q_out; k heads normalised and rotated and written straight into the k cache row
+ * of their slot; v heads copied into the v cache row of their slot (slots < 0 or >= num_slots are
+ * skipped, as ti_kv_append does). Bitwise what ti_qknorm_rope on q and k followed by ti_kv_append
+ * gives; no intermediate k tensor. Cache rows are [num_slots, cache_row_stride] with head h at
+ * h * head_dim.
+ */
+int ti_qknorm_rope_append(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k,
+                          int64_t k_stride_t, int64_t k_stride_h, const void* v,
+                          int64_t v_stride_t, int64_t v_stride_h, const void* q_weight,
+                          const void* k_weight, const void* cos, const void* sin,
+                          int64_t cs_stride_t, void* q_out, int64_t q_out_stride_t,
+                          int64_t q_out_stride_h, void* k_cache, void* v_cache,
+                          int64_t cache_row_stride, const int32_t* slot_mapping, int64_t num_slots,
+                          int32_t n_tokens, int32_t n_q_heads, int32_t n_kv_heads,
+                          int32_t head_dim, int32_t rotary_dim, float eps, int32_t dtype,
+                          void* stream);
+
+/*
+ * out[i] = a[i] * sigmoid(b[i]) for n (even) contiguous values, computed in fp32 and rounded to the
+ * storage type. Replaces fused_sigmoid_mul(a, b) (kernels/act_mul.py:62-79), the attention output
+ * gate of model/qwen_36.py:1083.
+ */
+int ti_sigmoid_mul(const void* a, const void* b, void* out, int64_t n, int32_t dtype,
+                   void* stream);
+
+/*
+ * ti_gqa_decode_paged with the sigmoid gate in its output epilogue:
+ *   out[b, h, :] = decode(b, h) * sigmoid(gate[b * gate_stride_b + h * gate_stride_h + :])
+ * bitwise what ti_gqa_decode_paged followed by ti_sigmoid_mul gives (decode output rounded to the
+ * storage type first, as the unfused pair does), without the extra pass over the output. The gate
+ * of model/qwen_36.py:1083 is q_gate [B, 1, H_q * D]: gate_stride_b = H_q * D, gate_stride_h = D.
+ * MFMA variant only (TI_DECODE_SCALAR returns TI_EUNSUPPORTED).
+ */
+int ti_gqa_decode_paged_gated(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                              const void* k_cache, const void* v_cache,
+                              const int32_t* block_table, int64_t block_table_stride,
+                              const int32_t* seqlen, void* out, void* workspace,
+                              int64_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+                              int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                              int64_t num_blocks, int32_t max_blocks_per_seq,
+                              int32_t split_tokens, int32_t variant, int32_t dtype,
+                              const void* gate, int64_t gate_stride_b, int64_t gate_stride_h,
+                              void* stream);
 
 /* Text of the last error reported on the calling thread ("" when none). */
 const char* ti_last_error(void);

@@ -103,3 +103,52 @@ def ref_gqa_prefill_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch
                             torch.zeros_like(acc))
             out[q0:q1, h, :] = o.to(q.dtype)
     return out
+
+
+def ref_qknorm_rope(x: torch.Tensor, weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                    eps: float = 1e-5) -> torch.Tensor:
+    """QK-norm + partial RoPE as the reference's fused kernel computes it, rows ``[..., D]``.
+
+    kernels/qknorm_rope.py:29-49: sum of squares in fp32, ``rsqrt(sum / D + eps)``, scale by
+    ``(1 + w)`` and round the normalised row to the input dtype (33-39); then for i < h =
+    rotary_dim/2, in fp32 from those rounded values, ``out[i] = y[i] c[i] - y[i+h] s[i]`` and
+    ``out[i+h] = y[i+h] c[i] + y[i] s[i]`` with ``c, s = cos/sin[:h]`` (41-48), rounded once; the
+    rest passes through. ``cos``/``sin`` are ``[rotary_dim]`` or ``[..tokens.., rotary_dim]``
+    broadcasting against ``x`` without its head axis (``x`` is ``[T, H, D]``).
+    """
+    d = x.shape[-1]
+    xf = x.float()
+    r = torch.rsqrt((xf * xf).sum(-1, keepdim=True) / d + eps)
+    y = (xf * r * (1.0 + weight.float())).to(x.dtype).float()
+    rd = cos.shape[-1]
+    half = rd // 2
+    if rd == 0:
+        return y.to(x.dtype)
+    c = cos[..., :half].float()
+    s = sin[..., :half].float()
+    if c.dim() == 2:          # per token: [T, half] -> [T, 1, half]
+        c, s = c.unsqueeze(1), s.unsqueeze(1)
+    y1, y2 = y[..., :half], y[..., half:rd]
+    out = torch.cat([y1 * c - y2 * s, y2 * c + y1 * s, y[..., rd:]], dim=-1)
+    return out.to(x.dtype)
+
+
+def ref_qknorm_rope_fp32(x: torch.Tensor, weight: torch.Tensor, cos: torch.Tensor,
+                         sin: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """The reference's own fp32 check of that kernel (kernels/qknorm_rope.py:58-84): everything in
+    fp32, ``mean(x^2)``, one rounding at the end. ``x`` ``[B, H, 1, D]``, cos/sin ``[B, 1, rd]``."""
+    xf = x.float()
+    xn = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
+    xn = (1.0 + weight.float()) * xn
+    rd = cos.shape[-1]
+    half = rd // 2
+    rot1, rot2 = xn[..., :half], xn[..., half:rd]
+    c = cos[..., :half].unsqueeze(2).float()
+    s = sin[..., :half].unsqueeze(2).float()
+    out = torch.cat([rot1 * c - rot2 * s, rot2 * c + rot1 * s, xn[..., rd:]], dim=-1)
+    return out.to(x.dtype)
+
+
+def ref_sigmoid_mul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``a * sigmoid(b)`` in fp32, rounded once (kernels/act_mul.py:81-114)."""
+    return (a.float() * torch.sigmoid(b.float())).to(a.dtype)

@@ -48,6 +48,19 @@ SIGNATURES = {
     "ti_paged_metadata": (ctypes.c_int, [_c_vp, _c_i64, _c_i32, _c_i32, _c_vp, _c_vp, _c_vp,
                                          _c_vp, _c_vp, _c_vp, _c_vp, _c_i32, _c_i32, _c_vp, _c_vp,
                                          _c_vp, _c_i64, _c_i32, _c_i32, _c_vp]),
+    "ti_qknorm_rope": (ctypes.c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_vp,
+                                      _c_vp, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
+                                      ctypes.c_float, _c_i32, _c_vp]),
+    "ti_qknorm_rope_append": (ctypes.c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp,
+                                             _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
+                                             _c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp,
+                                             _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                                             ctypes.c_float, _c_i32, _c_vp]),
+    "ti_sigmoid_mul": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i32, _c_vp]),
+    "ti_gqa_decode_paged_gated": (ctypes.c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_i64,
+                                                 _c_vp, _c_vp, _c_vp, _c_i64, _c_i32, _c_i32,
+                                                 _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32,
+                                                 _c_i32, _c_i32, _c_vp, _c_i64, _c_i64, _c_vp]),
     "ti_last_error": (ctypes.c_char_p, []),
     "ti_abi_version": (ctypes.c_int32, []),
 }

@@ -39,6 +39,27 @@ __device__ __forceinline__ uint32_t pack2(float x, float y, F16) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Two 16-bit values -> floats (exact), x in the low half.
+__device__ __forceinline__ float2 unpack2(uint32_t v, Bf16) {
+  return make_float2(__uint_as_float(v << 16), __uint_as_float(v & 0xffff0000u));
+}
+__device__ __forceinline__ float2 unpack2(uint32_t v, F16) {
+  const f16x2_t h = __builtin_bit_cast(f16x2_t, v);
+  return make_float2(float(h[0]), float(h[1]));
+}
+
+// Logistic function 1 / (1 + e^-x) through the HIP device library's expf.
+__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
+
+// a * sigmoid(g) for two packed 16-bit pairs, rounded back to the storage type: the output
+// epilogue of the sigmoid gate (out = attention output * sigmoid(gate)).
+template <typename Tag>
+__device__ __forceinline__ uint32_t gate_mul2(uint32_t a, uint32_t g, Tag tag) {
+  const float2 x = unpack2(a, tag);
+  const float2 y = unpack2(g, tag);
+  return pack2(x.x * sigmoidf(y.x), x.y * sigmoidf(y.y), tag);
+}
+
 __device__ __forceinline__ u32x4 load16(const uint16_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
@@ -97,6 +118,10 @@ struct DecodeArgs {
   // split_tokens), partials indexed [sequence][q-head][partition].
   int32_t balanced_wgs;
   int32_t chunk_min_tiles;  // lower bound on a balanced workgroup's run
+  // Optional sigmoid gate of the output (out = attention * sigmoid(gate)), [B, hq, D] at these
+  // strides; nullptr for the plain output.
+  const uint16_t* gate;
+  int64_t gate_sb, gate_sh;
 };
 
 

@@ -219,16 +219,23 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
   auto store_out = [&](int b) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     uint16_t* orow = a.out + (int64_t(b) * a.hq + h) * D;
+    const uint16_t* grow = a.gate ? a.gate + b * a.gate_sb + int64_t(h) * a.gate_sh : nullptr;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
+        const int d = 128 * c + 32 * g + 8 * r;
         u32x4 w;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           w[k] = pack2(o[8 * c + 2 * k][r] * inv, o[8 * c + 2 * k + 1][r] * inv, Tag{});
         }
-        *reinterpret_cast<u32x4*>(orow + 128 * c + 32 * g + 8 * r) = w;
+        if (grow) {
+          const u32x4 gv = load16(grow + d);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) w[k] = gate_mul2(w[k], gv[k], Tag{});
+        }
+        *reinterpret_cast<u32x4*>(orow + d) = w;
       }
     }
   };
@@ -340,6 +347,12 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
   const int lane = threadIdx.x;
   const int d0 = lane * PER;
   uint16_t* orow = a.out + (int64_t(b) * a.hq + h) * D + d0;
+  const uint16_t* grow = a.gate ? a.gate + b * a.gate_sb + int64_t(h) * a.gate_sh + d0 : nullptr;
+  // Writes one pair of output values, through the sigmoid gate when there is one.
+  auto put = [&](int j, uint32_t w) {
+    if (grow) w = gate_mul2(w, *reinterpret_cast<const uint32_t*>(grow + j), Tag{});
+    *reinterpret_cast<uint32_t*>(orow + j) = w;
+  };
   int64_t slot0 = 0, stride = 1;
   int nparts = 0;
   int first_part_slot1 = 0;  // balanced: the first part sits in slot 1 of its workgroup
@@ -352,7 +365,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
     const int nb = seq_tiles(a, b);
     if (nb == 0) {
 #pragma unroll
-      for (int j = 0; j < PER; j += 2) *reinterpret_cast<uint32_t*>(orow + j) = 0u;
+      for (int j = 0; j < PER; j += 2) put(j, 0u);
       return;
     }
     int tot = 0, pre = 0;
@@ -425,9 +438,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
-  for (int j = 0; j < PER; j += 2) {
-    *reinterpret_cast<uint32_t*>(orow + j) = pack2(acc[j] * inv, acc[j + 1] * inv, Tag{});
-  }
+  for (int j = 0; j < PER; j += 2) put(j, pack2(acc[j] * inv, acc[j + 1] * inv, Tag{}));
 }
 
 template <int D, typename Tag, int WPB>
@@ -579,16 +590,16 @@ extern "C" int ti_gqa_decode_plan(int32_t batch, int32_t num_q_heads, int32_t nu
   return TI_OK;
 }
 
-extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                                   const void* k_cache, const void* v_cache,
-                                   const int32_t* block_table, int64_t block_table_stride,
-                                   const int32_t* seqlen, void* out, void* workspace,
-                                   int64_t workspace_bytes, int32_t batch, int32_t num_q_heads,
-                                   int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
-                                   int64_t num_blocks, int32_t max_blocks_per_seq,
-                                   int32_t split_tokens, int32_t variant, int32_t dtype,
-                                   void* stream) {
-  using namespace ti;
+namespace ti {
+namespace {
+
+int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+                 const void* v_cache, const int32_t* block_table, int64_t block_table_stride,
+                 const int32_t* seqlen, void* out, void* workspace, int64_t workspace_bytes,
+                 int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                 int32_t page_size, int64_t num_blocks, int32_t max_blocks_per_seq,
+                 int32_t split_tokens, int32_t variant, int32_t dtype, const void* gate,
+                 int64_t gate_stride_b, int64_t gate_stride_h, void* stream) {
   if (dtype != TI_DTYPE_BF16 && dtype != TI_DTYPE_F16) {
     return fail(TI_EUNSUPPORTED, "ti_gqa_decode_paged: dtype code %d is not bf16/fp16", dtype);
   }
@@ -650,6 +661,18 @@ extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_
   a.max_splits = max_splits;
   a.split_tokens = split;
   a.scale_log2 = float(1.4426950408889634 / sqrt(double(head_dim)));
+  if (gate != nullptr) {
+    if (kind == TI_DECODE_SCALAR) {
+      return fail(TI_EUNSUPPORTED, "ti_gqa_decode_paged_gated: the gate epilogue is built for "
+                                   "the MFMA variant only");
+    }
+    if ((reinterpret_cast<uintptr_t>(gate) & 15) || gate_stride_b % 8 || gate_stride_h % 8) {
+      return fail(TI_EINVAL, "ti_gqa_decode_paged_gated: gate rows must be 16-byte aligned");
+    }
+  }
+  a.gate = static_cast<const uint16_t*>(gate);
+  a.gate_sb = gate_stride_b;
+  a.gate_sh = gate_stride_h;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf16 = dtype == TI_DTYPE_BF16;
   if (kind == TI_DECODE_SCALAR) {
@@ -673,4 +696,40 @@ extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_
   }
   return bf16 ? launch_decode<128, Bf16>(a, batch, reuse_kv, s)
               : launch_decode<128, F16>(a, batch, reuse_kv, s);
+}
+
+}  // namespace
+}  // namespace ti
+
+extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                   const void* k_cache, const void* v_cache,
+                                   const int32_t* block_table, int64_t block_table_stride,
+                                   const int32_t* seqlen, void* out, void* workspace,
+                                   int64_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+                                   int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                   int64_t num_blocks, int32_t max_blocks_per_seq,
+                                   int32_t split_tokens, int32_t variant, int32_t dtype,
+                                   void* stream) {
+  return ti::decode_entry(q, q_stride_b, q_stride_h, k_cache, v_cache, block_table,
+                          block_table_stride, seqlen, out, workspace, workspace_bytes, batch,
+                          num_q_heads, num_kv_heads, head_dim, page_size, num_blocks,
+                          max_blocks_per_seq, split_tokens, variant, dtype, nullptr, 0, 0, stream);
+}
+
+extern "C" int ti_gqa_decode_paged_gated(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+    const void* v_cache, const int32_t* block_table, int64_t block_table_stride,
+    const int32_t* seqlen, void* out, void* workspace, int64_t workspace_bytes, int32_t batch,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+    int64_t num_blocks, int32_t max_blocks_per_seq, int32_t split_tokens, int32_t variant,
+    int32_t dtype, const void* gate, int64_t gate_stride_b, int64_t gate_stride_h,
+    void* stream) {
+  if (batch > 0 && gate == nullptr) {
+    return ti::fail(TI_EINVAL, "ti_gqa_decode_paged_gated: null gate");
+  }
+  return ti::decode_entry(q, q_stride_b, q_stride_h, k_cache, v_cache, block_table,
+                          block_table_stride, seqlen, out, workspace, workspace_bytes, batch,
+                          num_q_heads, num_kv_heads, head_dim, page_size, num_blocks,
+                          max_blocks_per_seq, split_tokens, variant, dtype, gate, gate_stride_b,
+                          gate_stride_h, stream);
 }

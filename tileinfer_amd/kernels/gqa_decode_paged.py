@@ -59,6 +59,7 @@ def gqa_decode_paged_fn(
     split_tokens: int | None = None,
     variant: str = "auto",
     kv_reuse: bool = False,
+    gate: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Single-query paged GQA attention.
 
@@ -75,6 +76,10 @@ def gqa_decode_paged_fn(
             caching), so K/V keeps the default cache policy and shared pages hit in L2/MALL; the
             default streams every page once (``nt``), which is faster when nothing is shared.
             Results are bitwise identical either way.
+        gate: keyword-only; the attention output gate (model/qwen_36.py:1083), any tensor of
+            B * H_q * D values laid out [B, H_q, D] (``q_gate`` [B, 1, H_q * D] as the model has
+            it): the output is ``decode * sigmoid(gate)``, applied in the kernel's epilogue —
+            bitwise ``fused_sigmoid_mul(gqa_decode_paged_fn(...), gate)``.
     Returns:
         [B, H_q, D] tensor in q's dtype.
     """
@@ -132,11 +137,20 @@ def gqa_decode_paged_fn(
     _, _, ws_bytes = decode_plan(b, h_q, h_kv, d, page_size, width, split_tokens)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
     lib = _lib.load()
-    _lib.check(lib.ti_gqa_decode_paged(
-        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
-        block_table.data_ptr(), block_table.stride(0) if width > 0 else 0, seqlen_kv.data_ptr(),
-        out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes,
-        b, h_q, h_kv, d, page_size, rows // page_size, width, int(split_tokens or 0),
-        _VARIANTS[variant] | (_lib.TI_DECODE_REUSE_KV if kv_reuse else 0), code,
-        _lib.stream_handle(dev)))
+    args = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+            block_table.data_ptr(), block_table.stride(0) if width > 0 else 0,
+            seqlen_kv.data_ptr(), out.data_ptr(), ws.data_ptr() if ws is not None else None,
+            ws_bytes, b, h_q, h_kv, d, page_size, rows // page_size, width,
+            int(split_tokens or 0),
+            _VARIANTS[variant] | (_lib.TI_DECODE_REUSE_KV if kv_reuse else 0), code)
+    if gate is None:
+        _lib.check(lib.ti_gqa_decode_paged(*args, _lib.stream_handle(dev)))
+        return out
+    if gate.numel() != b * h_q * d or gate.dtype != dt or gate.device != dev:
+        raise ValueError(f"gate must hold {b}x{h_q}x{d} values of q's dtype on q's device")
+    g3 = gate.reshape(b, h_q, d)
+    if not _aligned_rows(g3):
+        g3 = g3.contiguous()
+    _lib.check(lib.ti_gqa_decode_paged_gated(*args, g3.data_ptr(), g3.stride(0), g3.stride(1),
+                                             _lib.stream_handle(dev)))
     return out
