@@ -47,6 +47,15 @@ constexpr int kKT = 32;  // keys per staged tile (two 16-key sub-tiles, each ins
 constexpr float kRescaleSlack = 8.f;  // exp2 units a row maximum may rise before O is rescaled
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// ds_read_b64_tr_b16 (measured on gfx950): within each 16-lane group, output lane j receives
+// element j % 4 of the 8-byte rows addressed by lanes j/4, j/4 + 4, j/4 + 8, j/4 + 12.
+__device__ __forceinline__ u32x2 lds_read_tr4(const uint16_t* p) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+}
 
 // LDS slot of 16-byte chunk c of K/V tile row r is c ^ lds_swizzle(r). On gfx950 a ds_read_b128
 // serves 16 lanes per cycle over 64 banks: lanes {0-3, 12-15, 20-23, 24-27} together, then
@@ -54,6 +63,11 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // this swizzle both MFMA operand reads of the tile -- K rows across lanes, V rows across
 // 16-lane groups -- hit 16 distinct bank quads per cycle, for head_dim 128 and 256.
 __device__ __forceinline__ int lds_swizzle(int r) { return (r ^ ((r << 1) & 8)) & 15; }
+
+// V tiles are read only by ds_read_b64_tr_b16, which serves 32 consecutive lanes per cycle (8 bytes
+// each, measured the same way); the V operand reads of one half-wave touch 8 rows, 4 lanes per 32
+// bytes of a row, so XOR-ing the chunk index with 2r puts every row's 32 bytes on distinct banks.
+__device__ __forceinline__ int lds_swizzle_v(int r) { return (2 * r) & 14; }
 
 // Max over the four 16-lane rows of the wave (lanes n, n+16, n+32, n+48).
 __device__ __forceinline__ float row_group_max(float x) {
@@ -81,7 +95,6 @@ __device__ __forceinline__ float row_group_sum(float x) {
 template <int D, int C, int W, typename Tag>
 __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int KK = D / 32;
-  constexpr int NC = D / 128;
   constexpr int NT = D / 16;
   constexpr int CPR = D / 8;              // 16-byte chunks per row
   constexpr int RPB = 1024 / (2 * D);     // rows per 1 KiB load (64 lanes x 16 bytes)
@@ -152,6 +165,23 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   // Keys up to this one are visible to every row of the wave.
   const int wave_first_key = a.causal ? offset + qb0 + (wave * 16 * C) / G : INT32_MAX;
 
+  // V^T operand addresses for the transposed reads, fixed for the whole kernel: lane (s, g)
+  // (s = lane % 16) points at key row 16h + 4g + s/4 and columns d0 + 4(s%4) .. +3, so the read
+  // gives output lane m the values V[16h + 4g + i][d0 + m], i = 0..3 -- the k-slots 8g + 4h + i
+  // of the A operand (keys 4g + i of sub-tile h, matching P). voff[h][dt % 8] is the element
+  // offset inside a stage of d-tile dt's piece; d-tiles dt and dt + 8 differ by 128 elements
+  // (the swizzle only permutes chunks inside each group of 16).
+  int voff[2][8];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int r = 16 * hh + 4 * g + (n >> 2);
+    const int sw = lds_swizzle_v(r);
+#pragma unroll
+    for (int dl = 0; dl < 8; ++dl) {
+      const int y = 2 * dl + ((n & 3) >> 1);
+      voff[hh][dl] = r * D + ((y ^ sw) * 8) + (n & 1) * 4;
+    }
+  }
   const uint32_t row_bytes = uint32_t(a.row_stride) * 2u;
   const int32_t* bt_row = a.block_table + int64_t(b) * a.bt_stride;
 
@@ -197,13 +227,15 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       const int blk = wave * LPW + i;                  // 1 KiB block of the tile (uniform)
       const int row = blk * RPB + lane / CPR;          // tile row of this lane's chunk
       const int slot = lane % CPR;
-      const int chunk = slot ^ lds_swizzle(row);
-      const uint32_t off = uint32_t(row & 15) * row_bytes + uint32_t(chunk) * 16u;
+      const int chunk_k = slot ^ lds_swizzle(row);
+      const int chunk_v = slot ^ lds_swizzle_v(row);
+      const uint32_t off_k = uint32_t(row & 15) * row_bytes + uint32_t(chunk_k) * 16u;
+      const uint32_t off_v = uint32_t(row & 15) * row_bytes + uint32_t(chunk_v) * 16u;
       const int sub = (blk * RPB) / 16;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(sub ? rk[1] : rk[0], (lds_ptr_t)(sk + blk * 512),
-                                               16, off, 0, 0, 0);
+                                               16, off_k, 0, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(sub ? rv[1] : rv[0], (lds_ptr_t)(sv + blk * 512),
-                                               16, off, 0, 0, 0);
+                                               16, off_v, 0, 0, 0);
     }
   };
 
@@ -289,31 +321,16 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       pop[c][2] = pack2(p[4], p[5], Tag{});
       pop[c][3] = pack2(p[6], p[7], Tag{});
     }
-    // O^T[16 d x 16 rows] += V^T[16 d x 32 keys] . P^T[32 keys x 16 rows]; k-slots 8g..8g+7 of a
-    // lane are keys 4g..4g+3 of sub-tile 0 then of sub-tile 1, for V and P alike.
+    // O^T[16 d x 16 rows] += V^T[16 d x 32 keys] . P^T[32 keys x 16 rows], d-tile dt covering
+    // d = 16 dt .. 16 dt + 15; the A operand comes from two transposed LDS reads.
 #pragma unroll
-    for (int cg = 0; cg < NC; ++cg) {
-      u32x4 vr[8];
+    for (int dt = 0; dt < NT; ++dt) {
+      const int dh = dt >> 3, dl = dt & 7;
+      const u32x2 lo = lds_read_tr4(sv + voff[0][dl] + 128 * dh);
+      const u32x2 hi = lds_read_tr4(sv + voff[1][dl] + 128 * dh);
+      const u32x4 vop = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int r0 = 4 * g + r, r1 = 16 + 4 * g + r;
-        vr[r] = *reinterpret_cast<const u32x4*>(sv + r0 * D + (((16 * cg + n) ^ lds_swizzle(r0)) * 8));
-        vr[4 + r] =
-            *reinterpret_cast<const u32x4*>(sv + r1 * D + (((16 * cg + n) ^ lds_swizzle(r1)) * 8));
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        u32x4 vop;
-        vop[0] = __builtin_amdgcn_perm(vr[1][e >> 1], vr[0][e >> 1], sel);
-        vop[1] = __builtin_amdgcn_perm(vr[3][e >> 1], vr[2][e >> 1], sel);
-        vop[2] = __builtin_amdgcn_perm(vr[5][e >> 1], vr[4][e >> 1], sel);
-        vop[3] = __builtin_amdgcn_perm(vr[7][e >> 1], vr[6][e >> 1], sel);
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-          o[c][8 * cg + e] = mfma16x16x32(vop, pop[c], o[c][8 * cg + e], Tag{});
-        }
-      }
+      for (int c = 0; c < C; ++c) o[c][dt] = mfma16x16x32(vop, pop[c], o[c][dt], Tag{});
     }
   };
 
@@ -349,17 +366,13 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     uint16_t* orow =
         a.out + int64_t(q_start + qb0 + tok) * a.o_st + int64_t(kvh * G + hh) * a.o_sh;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    // Lane (n, g) holds d = 16 dt + 4g .. +3 of its row in o[c][dt].
 #pragma unroll
-    for (int cg = 0; cg < NC; ++cg) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        u32x4 w;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          w[k] = pack2(o[c][8 * cg + 2 * k][r] * inv, o[c][8 * cg + 2 * k + 1][r] * inv, Tag{});
-        }
-        *reinterpret_cast<u32x4*>(orow + 128 * cg + 32 * g + 8 * r) = w;
-      }
+    for (int dt = 0; dt < NT; ++dt) {
+      u32x2 w;
+      w[0] = pack2(o[c][dt][0] * inv, o[c][dt][1] * inv, Tag{});
+      w[1] = pack2(o[c][dt][2] * inv, o[c][dt][3] * inv, Tag{});
+      *reinterpret_cast<u32x2*>(orow + 16 * dt + 4 * g) = w;
     }
   }
 }
