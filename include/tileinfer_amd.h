@@ -158,16 +158,33 @@ int ti_copy_blocks(const void* src, void* dst, const int64_t* block_pairs, int64
  *   seqlen_k     [batch] int32, clamped to max_blocks_per_seq * page_size
  *   out          [total_q, num_q_heads, head_dim], written for every row covered by cu_seqlens_q
  *   max_seqlen_q >= every q_len (rows past it are not computed)
- * One launch on `stream`, no workspace. head_dim 128 or 256; page_size a multiple of 16.
+ *   workspace    NULL (workspace_bytes ignored): one workgroup per (sequence, KV head, block of
+ *                query tokens), one launch; each row's result is then independent of the rest of
+ *                the batch and of how the prompt was chunked (bitwise). Otherwise, at least
+ *                ti_gqa_prefill_workspace_bytes() bytes, 256-byte aligned: a balanced schedule
+ *                gives every CU the same number of key tiles (units cut between workgroups are
+ *                merged in a fixed order; deterministic, but not batch-invariant); three launches
+ *                (schedule, attention, merge). The workspace is scratch of this call only.
+ * Launches on `stream`. head_dim 128 or 256; page_size a multiple of 16.
  */
 int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                          const void* k_cache, const void* v_cache, const int32_t* block_table,
                          int64_t block_table_stride, const int32_t* cu_seqlens_q,
                          const int32_t* seqlen_k, void* out, int64_t out_stride_t,
-                         int64_t out_stride_h, int32_t batch, int32_t total_q,
-                         int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
-                         int32_t head_dim, int32_t page_size, int64_t num_blocks,
-                         int32_t max_blocks_per_seq, int32_t causal, int32_t dtype, void* stream);
+                         int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
+                         int32_t batch, int32_t total_q, int32_t max_seqlen_q,
+                         int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                         int32_t page_size, int64_t num_blocks, int32_t max_blocks_per_seq,
+                         int32_t causal, int32_t dtype, void* stream);
+
+/*
+ * Workspace of the balanced ti_gqa_prefill_paged schedule for these sizes (host-only, no device
+ * work). *bytes_out = 0 when the call must run without one (more than 8192 sequences, or tile
+ * counts past int32). No reference counterpart (the reference's varlen kernel takes no workspace).
+ */
+int ti_gqa_prefill_workspace_bytes(int32_t batch, int32_t total_q, int32_t num_q_heads,
+                                   int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                   int32_t max_blocks_per_seq, int64_t* bytes_out);
 
 /*
  * Device-resident paged metadata for one step: persistent block tables updated in place, and the

@@ -111,7 +111,8 @@ def test_python_wrappers_validate_before_launch():
 def _prefill_abi(batch=1, total_q=4, max_q=4, hq=24, hkv=4, d=256, ps=16, dtype=0, ptr=None):
     lib = _lib.load()
     return lib.ti_gqa_prefill_paged(ptr, 24 * d, d, ptr, ptr, ptr, 8, ptr, ptr, ptr, 24 * d, d,
-                                    batch, total_q, max_q, hq, hkv, d, ps, 64, 8, 1, dtype, None)
+                                    None, 0, batch, total_q, max_q, hq, hkv, d, ps, 64, 8, 1,
+                                    dtype, None)
 
 
 def test_prefill_argument_errors_without_device():
@@ -123,6 +124,26 @@ def test_prefill_argument_errors_without_device():
     assert _prefill_abi(hq=25) == _lib.TI_EINVAL
     rc = _prefill_abi()
     assert rc == _lib.TI_EINVAL and b"null" in _lib.load().ti_last_error()
+
+
+def test_prefill_workspace_sizes():
+    """The balanced schedule's workspace: plan tables plus two partial slots of 128 rows (head_dim
+    256; 256 rows at 128) per resident workgroup; none past the schedule's sequence limit."""
+    lib = _lib.load()
+    out = ctypes.c_int64(-1)
+
+    def ws(batch, total_q, d=256, hq=24, hkv=4):
+        assert lib.ti_gqa_prefill_workspace_bytes(batch, total_q, hq, hkv, d, 16, 512,
+                                                  ctypes.byref(out)) == _lib.TI_OK
+        return out.value
+    one = ws(1, 2048)
+    assert one > 256 * 2 * 128 * 256 * 4            # at least one round of partial slots
+    assert ws(2, 2048) >= one                       # more pairs, more table rows
+    assert ws(8193, 9000) == 0                      # beyond the schedule: run without one
+    assert ws(1, 0) == 0
+    assert ws(4, 512, d=128, hq=16, hkv=2) > 0
+    assert lib.ti_gqa_prefill_workspace_bytes(1, 1, 24, 4, 96, 16, 8, ctypes.byref(out)) == \
+        _lib.TI_EUNSUPPORTED
 
 
 def test_missing_library_fails_loudly(tmp_path):

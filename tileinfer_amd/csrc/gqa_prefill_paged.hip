@@ -21,6 +21,8 @@
 //   S^T[16 keys x 16 rows]  = K[16 keys x 32 d] . Q^T[32 d x 16 rows]       (16x16x32, D/32 steps)
 //   O^T[16 d x 16 rows]    += V^T[16 d x 32 keys] . P^T[32 keys x 16 rows]   (16x16x32)
 // so each accumulator's query row is its lane's column and the softmax stays inside the lane.
+#include <atomic>
+
 #include "decode_common.h"
 
 namespace ti {
@@ -39,14 +41,27 @@ struct PrefillArgs {
   uint16_t* out;
   int64_t o_st, o_sh;
   int32_t total_q, num_blocks32, hq, hkv, group, page_size, max_blocks, causal;
-  int32_t tq;  // query tokens per workgroup: floor(64 * C / group)
+  int32_t tq;        // query tokens per unit: floor(rows per workgroup / group)
+  int32_t key_tile;  // keys per staged tile
   float scale_log2;
+  // Balanced schedule (balanced_wgs > 0; see prefill_plan_kernel), else one workgroup per unit.
+  int32_t balanced_wgs, max_pairs, min_chunk;
+  int32_t* plan;   // schedule tables
+  float* part_o;   // [balanced_wgs][2][rows][D] unnormalised partial rows
+  float* part_ml;  // [balanced_wgs][2][rows][2] their (m, l), m in exp2 units
 };
 
 // A staged tile holds NS 16-key sub-tiles (each inside one page): kKT = 16 * NS keys. Four
 // (64 keys) measured 1-3 % faster than two in a same-process A/B on MI355X.
 constexpr int kPrefillSubTiles = 4;
 constexpr float kRescaleSlack = 8.f;  // exp2 units a row maximum may rise before O is rescaled
+constexpr int kMinChunkTiles = 4;     // shortest run of key tiles of a balanced workgroup
+constexpr int kXcds = 8;              // MI355X: 8 XCDs of 32 CUs, one L2 each
+constexpr int kUnitCost = 2;          // a unit's start-up and epilogue, priced in key tiles
+static_assert(kMinChunkTiles > kUnitCost, "every balanced run must reach a key tile");
+// Instruction classes of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -85,10 +100,170 @@ __device__ __forceinline__ float row_group_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// One workgroup = one (sequence, KV head, block of tq query tokens); its rows are the
-// (token, query head) pairs of that KV head's group, row = token * group + head-in-group, 64*C rows
-// over 4 waves (C column tiles of 16 rows per wave). Every staged K/V tile is thus shared by all
-// query heads of the group, and every K/V operand read from LDS feeds C MFMAs.
+// Query and key extent of sequence b, clamped as the entry point documents.
+struct SeqExtent {
+  int q_start, q_len, kv_len;
+  int offset;  // query i sits at absolute position offset + i
+};
+
+__device__ __forceinline__ SeqExtent seq_extent(const PrefillArgs& a, int b) {
+  SeqExtent s;
+  s.q_start = min(max(a.cu_q[b], 0), a.total_q);
+  s.q_len = min(max(a.cu_q[b + 1], s.q_start), a.total_q) - s.q_start;
+  const int kv = a.seqlen_k[b];
+  const int cap = a.max_blocks * a.page_size;
+  s.kv_len = kv < 0 ? 0 : (kv > cap ? cap : kv);
+  s.offset = s.kv_len - s.q_len;
+  return s;
+}
+
+// Keys the query block starting at qb0 can see: j < kv_len, and j < offset + qb0 + tq under the
+// causal mask.
+__device__ __forceinline__ int block_key_end(const PrefillArgs& a, const SeqExtent& s, int qb0) {
+  const int tq = min(a.tq, s.q_len - qb0);
+  const int k_end = a.causal ? min(s.kv_len, s.offset + qb0 + tq) : s.kv_len;
+  return k_end < 0 ? 0 : k_end;
+}
+
+// Balanced schedule. A unit is (KV head, sequence, query block); its work is kUnitCost plus its key
+// tiles (the fixed part prices a unit's start-up and epilogue in tiles). Units are concatenated KV
+// head major, then by (sequence, query block) "pair", and workgroup i takes work [i * chunk,
+// (i + 1) * chunk) of the concatenation, so every workgroup gets the same work whatever the mix of
+// prompt and context lengths. A unit's key tiles sit at the end of its work; a unit cut between
+// workgroups is finished by each as an unnormalised partial (slot 0 when it is the workgroup's
+// first unit, 1 when its last) and merged afterwards in workgroup order. The tables, in the
+// workspace (int32):
+//   header   {pairs, work per KV head, chunk, total work}
+//   per pair {sequence, query block, key tiles, exclusive prefix of work}   (max_pairs each)
+//   per workgroup {KV head, pair, first key tile}                          (balanced_wgs each)
+struct PlanView {
+  int32_t *hdr, *pair_b, *pair_qb, *pair_nt, *pair_pre, *wg_kvh, *wg_p, *wg_t;
+};
+
+__device__ __forceinline__ PlanView plan_view(const PrefillArgs& a) {
+  PlanView v;
+  v.hdr = a.plan;
+  v.pair_b = a.plan + 4;
+  v.pair_qb = v.pair_b + a.max_pairs;
+  v.pair_nt = v.pair_qb + a.max_pairs;
+  v.pair_pre = v.pair_nt + a.max_pairs;
+  v.wg_kvh = v.pair_pre + a.max_pairs;
+  v.wg_p = v.wg_kvh + a.balanced_wgs;
+  v.wg_t = v.wg_p + a.balanced_wgs;
+  return v;
+}
+
+int64_t plan_ints(int64_t max_pairs, int64_t wgs) { return 4 + 4 * max_pairs + 3 * wgs; }
+
+constexpr int kPlanThreads = 1024;
+constexpr int kMaxPlanSeqs = 8192;  // sequences of one balanced launch (first pairs kept in LDS)
+
+__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+// Inclusive scan of x over the workgroup; `total` receives the workgroup's sum.
+__device__ int block_incl_scan(int x, int* s_w, int& total) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int incl = wave_incl_scan(x, lane);
+  if (lane == 63) s_w[w] = incl;
+  __syncthreads();
+  int pre = 0, tot = 0;
+  for (int i = 0; i < kPlanThreads / 64; ++i) {
+    const int y = s_w[i];
+    pre += i < w ? y : 0;
+    tot += y;
+  }
+  __syncthreads();  // s_w is reused by the next scan
+  total = tot;
+  return pre + incl;
+}
+
+// One workgroup builds the schedule tables from cu_seqlens_q / seqlen_k (device values, so the
+// launch sequence stays free of host reads).
+__global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs a, int batch) {
+  __shared__ int s_off[kMaxPlanSeqs + 1];
+  __shared__ int s_w[kPlanThreads / 64];
+  const int t = threadIdx.x;
+  const PlanView v = plan_view(a);
+  // First pair of every sequence (query blocks of the sequences before it).
+  int carry = 0;
+  for (int b0 = 0; b0 < batch; b0 += kPlanThreads) {
+    const int b = b0 + t;
+    const int nq = b < batch ? (seq_extent(a, b).q_len + a.tq - 1) / a.tq : 0;
+    int tot;
+    const int incl = block_incl_scan(nq, s_w, tot);
+    if (b < batch) s_off[b] = carry + incl - nq;
+    carry += tot;
+  }
+  if (t == 0) s_off[batch] = carry;
+  __syncthreads();
+  // Cannot exceed max_pairs for non-decreasing cu_seqlens_q; a malformed one loses the excess.
+  const int n_pairs = min(carry, a.max_pairs);
+  // Key tiles of every pair and the exclusive prefix of their work.
+  int work = 0;
+  for (int p0 = 0; p0 < n_pairs; p0 += kPlanThreads) {
+    const int p = p0 + t;
+    int nt = 0;
+    if (p < n_pairs) {
+      int lo = 0, hi = batch;  // s_off[lo] <= p < s_off[hi]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (s_off[mid] <= p) lo = mid;
+        else hi = mid;
+      }
+      const int qb = p - s_off[lo];
+      nt = (block_key_end(a, seq_extent(a, lo), qb * a.tq) + a.key_tile - 1) / a.key_tile;
+      v.pair_b[p] = lo;
+      v.pair_qb[p] = qb;
+      v.pair_nt[p] = nt;
+    }
+    const int w = nt > 0 ? nt + kUnitCost : 0;
+    int tot;
+    const int incl = block_incl_scan(w, s_w, tot);
+    if (p < n_pairs) v.pair_pre[p] = work + incl - w;
+    work += tot;
+  }
+  const int64_t total = int64_t(a.hkv) * work;
+  const int64_t wgs = a.balanced_wgs;
+  const int64_t chunk = max((total + wgs - 1) / wgs, int64_t(a.min_chunk));
+  if (t == 0) {
+    v.hdr[0] = n_pairs;
+    v.hdr[1] = work;
+    v.hdr[2] = int32_t(chunk);
+    v.hdr[3] = int32_t(total);
+  }
+  for (int i = t; i < wgs; i += kPlanThreads) v.wg_p[i] = -1;
+  __syncthreads();  // the -1 defaults land before the starts below
+  // Workgroup i starts in the unit holding work position i * chunk (units without key tiles
+  // hold none), at its first key tile when the position falls in the unit's fixed part.
+  const int units = a.hkv * n_pairs;
+  for (int u = t; u < units; u += kPlanThreads) {
+    const int kvh = u / n_pairs;
+    const int p = u - kvh * n_pairs;
+    const int nt = v.pair_nt[p];
+    if (nt == 0) continue;
+    const int64_t pre = int64_t(kvh) * work + v.pair_pre[p];
+    for (int64_t i = (pre + chunk - 1) / chunk; i <= (pre + kUnitCost + nt - 1) / chunk && i < wgs;
+         ++i) {
+      v.wg_kvh[i] = kvh;
+      v.wg_p[i] = p;
+      v.wg_t[i] = int32_t(max(i * chunk - pre - kUnitCost, int64_t(0)));
+    }
+  }
+}
+
+// A workgroup's rows are the (token, query head) pairs of one KV head's group, row = token * group
+// + head-in-group, 16 * C * W rows over W waves (C column tiles of 16 rows per wave). Every staged
+// K/V tile is thus shared by all query heads of the group, and every K/V operand read from LDS feeds
+// C MFMAs. Without a balanced schedule a workgroup is one unit (sequence, KV head, query block);
+// with one, it walks the units of its run of key tiles.
 //
 // K/V tiles go from the pages straight into LDS (buffer loads with the LDS destination), two
 // stages in distinct arrays so that the compiler's wait counting tells the stage being loaded from
@@ -102,6 +277,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int CPR = D / 8;              // 16-byte chunks per row
   constexpr int RPB = 1024 / (2 * D);     // rows per 1 KiB load (64 lanes x 16 bytes)
   constexpr int LPW = kKT / RPB / W;      // 1 KiB loads per wave per tile, each of K and V
+  constexpr int ROWS = 16 * C * W;        // rows of the workgroup
   static_assert(LPW * RPB * W == kKT && 16 % (kKT / W) == 0,
                 "each wave's loads must lie inside one sub-tile");
 
@@ -115,59 +291,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
-  const int kvh = blockIdx.x;
-  const int b = blockIdx.z;
   const int G = a.group;
-
-  const int q_start = min(max(a.cu_q[b], 0), a.total_q);
-  const int q_len = min(max(a.cu_q[b + 1], q_start), a.total_q) - q_start;
-  // Heaviest query blocks (latest tokens, longest causal range) are dispatched first.
-  const int qb0 = (gridDim.y - 1 - blockIdx.y) * a.tq;
-  if (qb0 >= q_len) return;  // uniform over the workgroup
-  int kv_len = a.seqlen_k[b];
-  const int cap = a.max_blocks * a.page_size;
-  kv_len = kv_len < 0 ? 0 : (kv_len > cap ? cap : kv_len);
-  const int offset = kv_len - q_len;  // query i sits at absolute position offset + i
-  const int tq = min(a.tq, q_len - qb0);
-
-  // This lane's C rows.
-  bool row_ok[C];
-  int q_pos[C];
-  u32x4 qop[C][KK];
-#pragma unroll
-  for (int c = 0; c < C; ++c) {
-    const int rho = wave * 16 * C + 16 * c + n;
-    const int tok = rho / G;
-    const int hh = rho - tok * G;
-    row_ok[c] = tok < tq;
-    q_pos[c] = a.causal ? offset + qb0 + tok : INT32_MAX;
-    const uint16_t* qrow =
-        a.q + int64_t(q_start + qb0 + tok) * a.q_st + int64_t(kvh * G + hh) * a.q_sh + 8 * g;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      qop[c][kk] = row_ok[c] ? load16(qrow + 32 * kk) : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-
-  f32x4 o[C][NT];
-  float m_run[C], l_run[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c) {
-#pragma unroll
-    for (int i = 0; i < NT; ++i) o[c][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    m_run[c] = -INFINITY;
-    l_run[c] = 0.f;
-  }
-
-  // Keys the workgroup can see: j < kv_len, and j < offset + qb0 + tq under the causal mask.
-  int k_end = a.causal ? min(kv_len, offset + qb0 + tq) : kv_len;
-  if (k_end < 0) k_end = 0;
-  const int ntiles = (k_end + kKT - 1) / kKT;
-  // Under the causal mask, keys past this one are masked for every row of the wave.
-  const int wave_tok = min(tq - 1, ((wave + 1) * 16 * C - 1) / G);
-  const int wave_last_key = a.causal ? offset + qb0 + wave_tok : INT32_MAX;
-  // Keys up to this one are visible to every row of the wave.
-  const int wave_first_key = a.causal ? offset + qb0 + (wave * 16 * C) / G : INT32_MAX;
 
   // V^T operand addresses for the transposed reads, fixed for the whole kernel: lane (s, g)
   // (s = lane % 16) points at key row 16h + 4g + s/4 and columns d0 + 4(s%4) .. +3, so the read
@@ -187,45 +311,55 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     }
   }
   const uint32_t row_bytes = uint32_t(a.row_stride) * 2u;
-  const int32_t* bt_row = a.block_table + int64_t(b) * a.bt_stride;
+  // The sub-tile this wave loads (kKT / W rows per wave, inside one sub-tile).
+  const int my_sub = (wave * (kKT / W)) / 16;
 
-  // Block ids of the next tile to load (uniform), fetched one tile ahead of their use.
-  int nbid[NS], nrows[NS];
-  auto load_ids = [&](int k0) {
+  // The current unit (uniform) and this lane's C rows of it.
+  int b = 0, kvh = 0, qb0 = 0;
+  SeqExtent sx;
+  const int32_t* bt_row = a.block_table;
+  int wave_last_key = 0, wave_first_key = 0;
+  bool row_ok[C];
+  int q_pos[C];
+  u32x4 qop[C][KK];
+  f32x4 o[C][NT];
+  float m_run[C], l_run[C];
+
+  // Block ids of the next tile to load (uniform), fetched one tile ahead of their use; -1 for a
+  // sub-tile with nothing to load (past the context, or an absent page: masked, never loaded).
+  int nbid[NS];
+  auto load_ids = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       const int key0 = k0 + 16 * j;
-      int rows = min(max(kv_len - key0, 0), 16);
-      int id = rows > 0 ? bt_row[key0 / a.page_size] : 0;
-      if (uint32_t(id) >= uint32_t(a.num_blocks32)) {
-        rows = 0;  // absent page: masked, never loaded
-        id = 0;
-      }
-      nbid[j] = id;
-      nrows[j] = rows;
+      const int id = key0 < sx.kv_len ? bt_row[key0 / a.page_size] : -1;
+      nbid[j] = uint32_t(id) < uint32_t(a.num_blocks32) ? id : -1;
     }
   };
-  // Rows of each sub-tile that exist in the two stages (uniform).
-  int rows_st[2][NS];
-  // The sub-tile this wave loads (kKT / W rows per wave, inside one sub-tile).
-  const int my_sub = (wave * (kKT / W)) / 16;
+  // Keys of the sub-tile at key0 that exist (uniform).
+  auto sub_rows = [&](int key0) __attribute__((always_inline)) {
+    return min(max(sx.kv_len - key0, 0), 16);
+  };
+  // Sub-tiles of each stage with nothing loaded (bit j; uniform). Kept as two masks rather than
+  // per-sub-tile row counts: the tile loop is short of scalar registers.
+  uint32_t empty_st[2];
   // Issue this wave's loads of the tile at key k0 into stage (sk, sv). A sub-tile lies in one
   // page; its loads use a buffer descriptor spanning only the rows that exist, so rows past the
   // context or in an absent page land in LDS as zero without a memory access.
-  auto fetch = [&](uint16_t* sk, uint16_t* sv, int (&rows_out)[NS], int k0) {
-    int bid = nbid[0], rows = nrows[0];
+  auto fetch = [&](uint16_t* sk, uint16_t* sv, uint32_t& empty_out, int k0)
+      __attribute__((always_inline)) {
+    int bid = nbid[0];
+    uint32_t empty = nbid[0] < 0 ? 1u : 0u;
 #pragma unroll
     for (int j = 1; j < NS; ++j) {
-      if (my_sub == j) {
-        bid = nbid[j];
-        rows = nrows[j];
-      }
+      if (my_sub == j) bid = nbid[j];
+      empty |= (nbid[j] < 0 ? 1u : 0u) << j;
     }
-#pragma unroll
-    for (int j = 0; j < NS; ++j) rows_out[j] = nrows[j];
+    empty_out = empty;
     bid = __builtin_amdgcn_readfirstlane(bid);
-    rows = __builtin_amdgcn_readfirstlane(rows);
     const int key0 = k0 + 16 * my_sub;
+    const int rows = __builtin_amdgcn_readfirstlane(bid < 0 ? 0 : sub_rows(key0));
+    bid = bid < 0 ? 0 : bid;
     const int64_t base = int64_t(bid) * a.page_stride +
                          int64_t(key0 % a.page_size) * a.row_stride + int64_t(kvh) * D;
     const uint32_t nbytes = rows > 0 ? uint32_t(rows - 1) * row_bytes + D * 2 : 0u;
@@ -245,7 +379,8 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     }
   };
 
-  auto compute = [&](const uint16_t* sk, const uint16_t* sv, const int (&rows_in)[NS], int k0) {
+  auto compute = [&](const uint16_t* sk, const uint16_t* sv, uint32_t empty, int k0)
+      __attribute__((always_inline)) {
     // S^T of each sub-tile that holds a key some row of the wave can see; the rest stay zero.
     f32x4 s[NS][C];
     int rows[NS];
@@ -255,7 +390,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       for (int c = 0; c < C; ++c) s[j][c] = f32x4{0.f, 0.f, 0.f, 0.f};
       rows[j] = 0;
       if (k0 + 16 * j <= wave_last_key) {  // uniform
-        rows[j] = rows_in[j];
+        rows[j] = ((empty >> j) & 1u) ? 0 : sub_rows(k0 + 16 * j);
         u32x4 kop[KK];
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
@@ -330,84 +465,401 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     }
     // O^T[16 d x 16 rows] += V^T[16 d x 32 keys] . P^T[32 keys x 16 rows] per pair of sub-tiles,
     // d-tile dt covering d = 16 dt .. 16 dt + 15; the A operand comes from two transposed reads.
+    // The reads run two d-tiles ahead of the MFMAs; the scheduling barriers keep that order (left
+    // to itself the scheduler may serialise each read with its MFMA when scalar registers run
+    // short).
 #pragma unroll
     for (int h = 0; h < NS / 2; ++h) {
       if (k0 + 32 * h > wave_last_key) continue;  // uniform: every P of the pair is zero
+      const uint16_t* svh = sv + 32 * h * D;
+      auto read_v = [&](int dt) __attribute__((always_inline)) {
+        const int dh = dt >> 3, dl = dt & 7;
+        const u32x2 lo = lds_read_tr4(svh + voff[0][dl] + 128 * dh);
+        const u32x2 hi = lds_read_tr4(svh + voff[1][dl] + 128 * dh);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+      u32x4 vop[3];
+      vop[0] = read_v(0);
+      vop[1] = read_v(1);
 #pragma unroll
       for (int dt = 0; dt < NT; ++dt) {
-        const int dh = dt >> 3, dl = dt & 7;
-        const u32x2 lo = lds_read_tr4(sv + 32 * h * D + voff[0][dl] + 128 * dh);
-        const u32x2 hi = lds_read_tr4(sv + 32 * h * D + voff[1][dl] + 128 * dh);
-        const u32x4 vop = {lo[0], lo[1], hi[0], hi[1]};
+        __builtin_amdgcn_sched_barrier(0);
+        if (dt + 2 < NT) vop[(dt + 2) % 3] = read_v(dt + 2);
 #pragma unroll
-        for (int c = 0; c < C; ++c) o[c][dt] = mfma16x16x32(vop, pop[c][h], o[c][dt], Tag{});
+        for (int c = 0; c < C; ++c) {
+          o[c][dt] = mfma16x16x32(vop[dt % 3], pop[c][h], o[c][dt], Tag{});
+        }
       }
     }
   };
 
-  if (ntiles > 0) {
-    load_ids(0);
-    fetch(sk0, sv0, rows_st[0], 0);
-    if (ntiles > 1) load_ids(kKT);
-  }
-  // Two tiles per trip so that each stage is a compile-time array.
-  for (int it = 0; it < ntiles; it += 2) {
-    __syncthreads();  // stage 0 holds tile it; every wave is done with stage 1
-    if (it + 1 < ntiles) {
-      fetch(sk1, sv1, rows_st[1], (it + 1) * kKT);
-      if (it + 2 < ntiles) load_ids((it + 2) * kKT);
+  // Attention of unit (b, kvh, qb0) over its key tiles [t0, t1): leaves the unnormalised o and
+  // the per-lane m_run / l_run. Uniform over the workgroup.
+  auto run_unit = [&](int t0, int t1) __attribute__((always_inline)) {
+    sx = seq_extent(a, b);
+    sx.q_start = __builtin_amdgcn_readfirstlane(sx.q_start);
+    sx.q_len = __builtin_amdgcn_readfirstlane(sx.q_len);
+    sx.kv_len = __builtin_amdgcn_readfirstlane(sx.kv_len);
+    sx.offset = __builtin_amdgcn_readfirstlane(sx.offset);
+    const int tq = min(a.tq, sx.q_len - qb0);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int rho = wave * 16 * C + 16 * c + n;
+      const int tok = rho / G;
+      const int hh = rho - tok * G;
+      row_ok[c] = tok < tq;
+      q_pos[c] = a.causal ? sx.offset + qb0 + tok : INT32_MAX;
+      const uint16_t* qrow = a.q + int64_t(sx.q_start + qb0 + tok) * a.q_st +
+                             int64_t(kvh * G + hh) * a.q_sh + 8 * g;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        qop[c][kk] = row_ok[c] ? load16(qrow + 32 * kk) : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int i = 0; i < NT; ++i) o[c][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m_run[c] = -INFINITY;
+      l_run[c] = 0.f;
     }
-    if (it * kKT <= wave_last_key) compute(sk0, sv0, rows_st[0], it * kKT);
-    if (it + 1 >= ntiles) break;
-    __syncthreads();  // stage 1 holds tile it + 1; every wave is done with stage 0
-    if (it + 2 < ntiles) {
-      fetch(sk0, sv0, rows_st[0], (it + 2) * kKT);
-      if (it + 3 < ntiles) load_ids((it + 3) * kKT);
+    // Under the causal mask, keys past wave_last_key are masked for every row of the wave and
+    // keys up to wave_first_key are visible to all of them.
+    const int wave_tok = min(tq - 1, ((wave + 1) * 16 * C - 1) / G);
+    wave_last_key = a.causal ? sx.offset + qb0 + wave_tok : INT32_MAX;
+    wave_first_key = a.causal ? sx.offset + qb0 + (wave * 16 * C) / G : INT32_MAX;
+    bt_row = a.block_table + int64_t(b) * a.bt_stride;
+    const int cnt = t1 - t0;
+    if (cnt > 0) load_ids(t0 * kKT);
+    // Every wave is done reading both stages (previous unit). LDS only: the previous unit's
+    // output stores may still be in flight; they drain under this unit's first loads.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (cnt > 0) {
+      fetch(sk0, sv0, empty_st[0], t0 * kKT);
+      if (cnt > 1) load_ids((t0 + 1) * kKT);
     }
-    if ((it + 1) * kKT <= wave_last_key) compute(sk1, sv1, rows_st[1], (it + 1) * kKT);
-  }
+    // Two tiles per trip so that each stage is a compile-time array.
+    for (int it = 0; it < cnt; it += 2) {
+      const int k0 = (t0 + it) * kKT;
+      __syncthreads();  // stage 0 holds tile it; every wave is done with stage 1
+      if (it + 1 < cnt) {
+        fetch(sk1, sv1, empty_st[1], k0 + kKT);
+        if (it + 2 < cnt) load_ids(k0 + 2 * kKT);
+      }
+      if (k0 <= wave_last_key) compute(sk0, sv0, empty_st[0], k0);
+      if (it + 1 >= cnt) break;
+      __syncthreads();  // stage 1 holds tile it + 1; every wave is done with stage 0
+      if (it + 2 < cnt) {
+        fetch(sk0, sv0, empty_st[0], k0 + 2 * kKT);
+        if (it + 3 < cnt) load_ids(k0 + 3 * kKT);
+      }
+      if (k0 + kKT <= wave_last_key) compute(sk1, sv1, empty_st[1], k0 + kKT);
+    }
+  };
 
+  // The unit's normalised rows into `out`.
+  auto store_final = [&]() __attribute__((always_inline)) {
 #pragma unroll
-  for (int c = 0; c < C; ++c) {
-    const float l_tot = row_group_sum(l_run[c]);
-    if (!row_ok[c]) continue;
-    const int rho = wave * 16 * C + 16 * c + n;
-    const int tok = rho / G;
-    const int hh = rho - tok * G;
-    uint16_t* orow =
-        a.out + int64_t(q_start + qb0 + tok) * a.o_st + int64_t(kvh * G + hh) * a.o_sh;
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    // Lane (n, g) holds d = 16 dt + 4g .. +3 of its row in o[c][dt].
+    for (int c = 0; c < C; ++c) {
+      const float l_tot = row_group_sum(l_run[c]);
+      if (!row_ok[c]) continue;
+      const int rho = wave * 16 * C + 16 * c + n;
+      const int tok = rho / G;
+      const int hh = rho - tok * G;
+      uint16_t* orow =
+          a.out + int64_t(sx.q_start + qb0 + tok) * a.o_st + int64_t(kvh * G + hh) * a.o_sh;
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+      // Lane (n, g) holds d = 16 dt + 4g .. +3 of its row in o[c][dt].
 #pragma unroll
-    for (int dt = 0; dt < NT; ++dt) {
-      u32x2 w;
-      w[0] = pack2(o[c][dt][0] * inv, o[c][dt][1] * inv, Tag{});
-      w[1] = pack2(o[c][dt][2] * inv, o[c][dt][3] * inv, Tag{});
-      *reinterpret_cast<u32x2*>(orow + 16 * dt + 4 * g) = w;
+      for (int dt = 0; dt < NT; ++dt) {
+        u32x2 w;
+        w[0] = pack2(o[c][dt][0] * inv, o[c][dt][1] * inv, Tag{});
+        w[1] = pack2(o[c][dt][2] * inv, o[c][dt][3] * inv, Tag{});
+        *reinterpret_cast<u32x2*>(orow + 16 * dt + 4 * g) = w;
+      }
+    }
+  };
+
+  // The unit's unnormalised rows (o relative to 2^m, with m and the row's l) into partial slot
+  // rows [row0, row0 + ROWS).
+  auto store_partial = [&](int64_t row0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const float l_tot = row_group_sum(l_run[c]);
+      if (!row_ok[c]) continue;
+      const int64_t r = row0 + wave * 16 * C + 16 * c + n;
+      float* prow = a.part_o + r * D + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < NT; ++dt) *reinterpret_cast<f32x4*>(prow + 16 * dt) = o[c][dt];
+      if (g == 0) {
+        a.part_ml[2 * r] = m_run[c];
+        a.part_ml[2 * r + 1] = l_tot;
+      }
+    }
+  };
+
+  // Work of this workgroup: one unit, or (balanced) a run of key tiles over consecutive units.
+  // One call site per lambda keeps every per-lane array in registers.
+  const bool balanced = a.balanced_wgs > 0;
+  // Balanced runs are dealt to the XCDs in contiguous blocks: workgroup ids go round-robin over
+  // the 8 XCDs, so run i = (id % 8) * (G / 8) + id / 8 keeps consecutive runs (one KV head,
+  // neighbouring query blocks, the same K/V pages) in one XCD's L2.
+  const int nwg = a.balanced_wgs;
+  const int i = (nwg % kXcds == 0) ? int(blockIdx.x % kXcds) * (nwg / kXcds) + int(blockIdx.x / kXcds)
+                                   : int(blockIdx.x);
+  const PlanView v = plan_view(a);
+  int p = 0, n_pairs = 1, grid_nt = 0, unit_work = 1;
+  int64_t pos = 0, end = 0;  // this workgroup's work positions (balanced)
+  if (!balanced) {
+    // The heaviest query blocks (latest tokens, longest causal range) are dispatched first.
+    kvh = blockIdx.x;
+    b = blockIdx.z;
+    qb0 = (gridDim.y - 1 - blockIdx.y) * a.tq;
+    const SeqExtent s0 = seq_extent(a, b);
+    if (qb0 >= s0.q_len) return;  // uniform over the workgroup
+    grid_nt = (block_key_end(a, s0, qb0) + kKT - 1) / kKT;
+  } else {
+    p = __builtin_amdgcn_readfirstlane(v.wg_p[i]);
+    if (p < 0) return;  // no work left for this workgroup
+    kvh = __builtin_amdgcn_readfirstlane(v.wg_kvh[i]);
+    n_pairs = __builtin_amdgcn_readfirstlane(v.hdr[0]);
+    unit_work = __builtin_amdgcn_readfirstlane(v.hdr[1]);
+    const int64_t chunk = __builtin_amdgcn_readfirstlane(v.hdr[2]);
+    const int64_t total = __builtin_amdgcn_readfirstlane(v.hdr[3]);
+    pos = int64_t(i) * chunk;
+    end = min(pos + chunk, total);
+  }
+  bool first = true;
+  for (;;) {
+    int nt = grid_nt, t0 = 0, t1 = grid_nt;
+    bool last = true;
+    if (balanced) {
+      nt = __builtin_amdgcn_readfirstlane(v.pair_nt[p]);
+      b = __builtin_amdgcn_readfirstlane(v.pair_b[p]);
+      qb0 = __builtin_amdgcn_readfirstlane(v.pair_qb[p]) * a.tq;
+      // The unit's key tiles occupy work [k_pos, k_pos + nt); this run covers [pos, end).
+      const int64_t k_pos = int64_t(kvh) * unit_work +
+                            __builtin_amdgcn_readfirstlane(v.pair_pre[p]) + kUnitCost;
+      t0 = int(max(pos - k_pos, int64_t(0)));
+      t1 = int(min(end - k_pos, int64_t(nt)));
+      last = k_pos + nt >= end;
+    }
+    // Units without keys get their zero rows from the merge (balanced) or here (grid: nt = 0).
+    if (t0 < t1 || !balanced) {
+      run_unit(t0, t1);
+      if (t0 == 0 && t1 == nt) store_final();
+      else store_partial((int64_t(i) * 2 + (first ? 0 : 1)) * ROWS);
+      first = false;
+    }
+    if (last) break;
+    if (++p == n_pairs) {
+      p = 0;
+      if (++kvh == a.hkv) break;
     }
   }
 }
 
-template <int D, int C, int W, int NS>
-void launch_prefill(const PrefillArgs& a0, int batch, int max_q, bool bf16, hipStream_t s) {
+// Combines the partials of every unit that was cut between workgroups, in workgroup order, and
+// writes the zero rows of units with no visible key: per row m = max m_s, w_s = 2^(m_s - m),
+// out = sum w_s o_s / sum w_s l_s. One workgroup per (pair, KV head, block of kMergeRows rows);
+// each thread takes 8 values of kMergeRowsPerThread rows, loads first, so that their latencies
+// overlap.
+constexpr int kMergeRowsPerThread = 1;
+
+template <int D, int ROWS, typename Tag>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
+  constexpr int TPR = D / 8;                          // threads per row, 8 values each
+  constexpr int RPT = kMergeRowsPerThread;
+  constexpr int RPW = 256 / TPR * RPT;                // rows per workgroup
+  const PlanView v = plan_view(a);
+  const int p = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int n_pairs = v.hdr[0];
+  if (p >= n_pairs) return;
+  const int unit_work = v.hdr[1];
+  const int64_t chunk = v.hdr[2];
+  const int b = v.pair_b[p];
+  const int qb0 = v.pair_qb[p] * a.tq;
+  const int nt = v.pair_nt[p];
+  int64_t i0 = 0;
+  int nparts = 0, first_slot = 0;
+  if (nt > 0) {
+    const int64_t pre = int64_t(kvh) * unit_work + v.pair_pre[p];
+    const int64_t k_pos = pre + kUnitCost;  // work position of the unit's first key tile
+    i0 = k_pos / chunk;
+    const int64_t i1 = (k_pos + nt - 1) / chunk;
+    if (i0 == i1) return;  // one workgroup finished the unit
+    nparts = int(i1 - i0 + 1);
+    // The first part is slot 1 of a workgroup that started in an earlier unit.
+    first_slot = i0 * chunk < pre ? 1 : 0;
+  }
+  const SeqExtent sx = seq_extent(a, b);
+  const int rows = min(a.tq, sx.q_len - qb0) * a.group;
+  const int d0 = (threadIdx.x % TPR) * 8;
+  const int r0 = int(blockIdx.z) * RPW + int(threadIdx.x) / TPR;  // rows r0 + j * (256 / TPR)
+  if (r0 >= rows) return;
+  auto part_row = [&](int s, int j) -> int64_t {
+    return ((i0 + s) * 2 + (s == 0 ? first_slot : 0)) * ROWS + r0 + j * (256 / TPR);
+  };
+  float m[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) m[j] = -INFINITY;
+  for (int s = 0; s < nparts; ++s) {
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) m[j] = fmaxf(m[j], a.part_ml[2 * part_row(s, j)]);
+  }
+  f32x4 acc[RPT][2];
+  float l[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    acc[j][0] = acc[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    l[j] = 0.f;
+  }
+  for (int s = 0; s < nparts; ++s) {
+    float ms[RPT], ls[RPT];
+    f32x4 x[RPT][2];
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const int64_t pr = part_row(s, j);
+      ms[j] = a.part_ml[2 * pr];
+      ls[j] = a.part_ml[2 * pr + 1];
+      const f32x4* src = reinterpret_cast<const f32x4*>(a.part_o + pr * D + d0);
+      x[j][0] = src[0];
+      x[j][1] = src[1];
+    }
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const float w = ms[j] == -INFINITY ? 0.f : fast_exp2(ms[j] - m[j]);
+      l[j] += w * ls[j];
+      acc[j][0] += w * x[j][0];
+      acc[j][1] += w * x[j][1];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int r = r0 + j * (256 / TPR);
+    if (r >= rows) break;
+    const float inv = l[j] > 0.f ? 1.f / l[j] : 0.f;
+    const int tok = r / a.group;
+    const int hh = r - tok * a.group;
+    uint16_t* orow = a.out + int64_t(sx.q_start + qb0 + tok) * a.o_st +
+                     int64_t(kvh * a.group + hh) * a.o_sh + d0;
+    u32x4 w;
+    w[0] = pack2(acc[j][0][0] * inv, acc[j][0][1] * inv, Tag{});
+    w[1] = pack2(acc[j][0][2] * inv, acc[j][0][3] * inv, Tag{});
+    w[2] = pack2(acc[j][1][0] * inv, acc[j][1][1] * inv, Tag{});
+    w[3] = pack2(acc[j][1][2] * inv, acc[j][1][3] * inv, Tag{});
+    *reinterpret_cast<u32x4*>(orow) = w;
+  }
+}
+
+// Launch shape per head_dim: C column tiles per wave, W waves.
+template <int D> struct PrefillShape;
+template <> struct PrefillShape<256> { static constexpr int C = 1, W = 8; };
+template <> struct PrefillShape<128> { static constexpr int C = 2, W = 8; };
+
+int prefill_rows(int head_dim) { return head_dim == 256 ? 16 * 1 * 8 : 16 * 2 * 8; }
+
+// Workgroups of one balanced launch: every CU's resident workgroups (one round).
+template <int D, typename Tag>
+int balanced_wgs() {
+  using S = PrefillShape<D>;
+  static std::atomic<int> cached{0};  // same code object on every gfx950 device
+  int per_cu = cached.load(std::memory_order_relaxed);
+  if (per_cu == 0) {
+    const auto fn = prefill_mfma_kernel<D, S::C, S::W, kPrefillSubTiles, Tag>;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
+                                                     64 * S::W, 0) != hipSuccess || per_cu <= 0) {
+      (void)hipGetLastError();
+      per_cu = 1;
+    }
+    cached.store(per_cu, std::memory_order_relaxed);
+  }
+  return device_cu_count() * per_cu;
+}
+
+// Upper bound of balanced_wgs (LDS bounds the resident workgroups per CU).
+int balanced_wgs_bound(int head_dim) {
+  const int lds = 4 * 16 * kPrefillSubTiles * head_dim * 2;
+  return device_cu_count() * (160 * 1024 / lds);
+}
+
+template <int D, typename Tag>
+int launch_prefill(const PrefillArgs& a0, int batch, int max_q, hipStream_t s) {
+  using S = PrefillShape<D>;
   PrefillArgs a = a0;
-  a.tq = (16 * C * W) / a.group;
-  const dim3 grid(unsigned(a.hkv), unsigned(ceil_div(max_q, a.tq)), unsigned(batch));
-  if (bf16) hipLaunchKernelGGL((prefill_mfma_kernel<D, C, W, NS, Bf16>), grid, dim3(64 * W), 0, s, a);
-  else hipLaunchKernelGGL((prefill_mfma_kernel<D, C, W, NS, F16>), grid, dim3(64 * W), 0, s, a);
+  const auto kern = prefill_mfma_kernel<D, S::C, S::W, kPrefillSubTiles, Tag>;
+  if (a.balanced_wgs == 0) {
+    const dim3 grid(unsigned(a.hkv), unsigned(ceil_div(max_q, a.tq)), unsigned(batch));
+    hipLaunchKernelGGL(kern, grid, dim3(64 * S::W), 0, s, a);
+    return check_launch("ti_gqa_prefill_paged");
+  }
+  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, a, batch);
+  int rc = check_launch("ti_gqa_prefill_paged (plan)");
+  if (rc != TI_OK) return rc;
+  hipLaunchKernelGGL(kern, dim3(unsigned(a.balanced_wgs)), dim3(64 * S::W), 0, s, a);
+  rc = check_launch("ti_gqa_prefill_paged");
+  if (rc != TI_OK) return rc;
+  constexpr int kRows = 16 * S::C * S::W;
+  constexpr int kMergeRows = 256 / (D / 8) * kMergeRowsPerThread;  // rows per merge workgroup
+  static_assert(kRows % kMergeRows == 0, "merge row blocks must tile the unit");
+  hipLaunchKernelGGL((prefill_merge_kernel<D, kRows, Tag>),
+                     dim3(unsigned(a.max_pairs), unsigned(a.hkv), unsigned(kRows / kMergeRows)),
+                     dim3(256), 0, s, a);
+  return check_launch("ti_gqa_prefill_paged (merge)");
+}
+
+// Balanced-schedule sizes of one call; false when the call runs one workgroup per unit (too many
+// sequences for the schedule's tables, or tile counts beyond int32).
+bool balanced_sizes(int32_t batch, int32_t total_q, int32_t hq, int32_t hkv, int32_t head_dim,
+                    int32_t page_size, int32_t max_blocks, int64_t wgs, int64_t* max_pairs,
+                    int64_t* bytes) {
+  if (batch <= 0 || batch > kMaxPlanSeqs || hkv <= 0 || hq % hkv != 0) return false;
+  const int64_t tq = prefill_rows(head_dim) / (hq / hkv);
+  if (tq <= 0) return false;
+  const int64_t pairs = ceil_div(total_q, tq) + batch;
+  const int64_t kt = 16 * kPrefillSubTiles;
+  const int64_t tiles_bound =
+      pairs * (ceil_div(int64_t(max_blocks) * page_size, kt) + kUnitCost) * hkv;
+  if (pairs > INT32_MAX / 8 || tiles_bound > INT32_MAX / 2 || hkv * pairs > INT32_MAX / 2) {
+    return false;
+  }
+  const int64_t ints = (plan_ints(pairs, wgs) + 63) / 64 * 64;  // 256-byte aligned floats after
+  const int64_t rows = int64_t(wgs) * 2 * prefill_rows(head_dim);
+  *max_pairs = pairs;
+  *bytes = ints * 4 + rows * (head_dim + 2) * 4;
+  return true;
 }
 
 }  // namespace
 }  // namespace ti
+
+extern "C" int ti_gqa_prefill_workspace_bytes(int32_t batch, int32_t total_q, int32_t num_q_heads,
+                                              int32_t num_kv_heads, int32_t head_dim,
+                                              int32_t page_size, int32_t max_blocks_per_seq,
+                                              int64_t* bytes_out) {
+  using namespace ti;
+  if (!bytes_out) return fail(TI_EINVAL, "ti_gqa_prefill_workspace_bytes: null output pointer");
+  if (head_dim != 128 && head_dim != 256) {
+    return fail(TI_EUNSUPPORTED, "ti_gqa_prefill_workspace_bytes: head_dim %d not built",
+                head_dim);
+  }
+  int64_t pairs = 0, bytes = 0;
+  if (total_q <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || page_size <= 0 ||
+      max_blocks_per_seq < 0 ||
+      !balanced_sizes(batch, total_q, num_q_heads, num_kv_heads, head_dim, page_size,
+                      max_blocks_per_seq, balanced_wgs_bound(head_dim), &pairs, &bytes)) {
+    bytes = 0;
+  }
+  *bytes_out = bytes;
+  return TI_OK;
+}
 
 extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                                     const void* k_cache, const void* v_cache,
                                     const int32_t* block_table, int64_t block_table_stride,
                                     const int32_t* cu_seqlens_q, const int32_t* seqlen_k,
                                     void* out, int64_t out_stride_t, int64_t out_stride_h,
-                                    int32_t batch, int32_t total_q, int32_t max_seqlen_q,
-                                    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                                    int32_t page_size,
+                                    void* workspace, int64_t workspace_bytes, int32_t batch,
+                                    int32_t total_q, int32_t max_seqlen_q, int32_t num_q_heads,
+                                    int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                                     int64_t num_blocks, int32_t max_blocks_per_seq, int32_t causal,
                                     int32_t dtype, void* stream) {
   using namespace ti;
@@ -415,7 +867,8 @@ extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q
     return fail(TI_EUNSUPPORTED, "ti_gqa_prefill_paged: dtype code %d is not bf16/fp16", dtype);
   }
   if (batch < 0 || total_q < 0 || max_seqlen_q < 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
-      num_q_heads % num_kv_heads != 0 || max_blocks_per_seq < 0 || num_blocks < 0) {
+      num_q_heads % num_kv_heads != 0 || max_blocks_per_seq < 0 || num_blocks < 0 ||
+      workspace_bytes < 0) {
     return fail(TI_EINVAL, "ti_gqa_prefill_paged: bad sizes");
   }
   if (num_q_heads / num_kv_heads > 64) {
@@ -437,9 +890,11 @@ extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q
   if (block_table_stride < max_blocks_per_seq || q_stride_h % 8 || q_stride_t % 8 ||
       out_stride_h % 8 || out_stride_t % 8 || (reinterpret_cast<uintptr_t>(q) & 15) ||
       (reinterpret_cast<uintptr_t>(out) & 15) || (reinterpret_cast<uintptr_t>(k_cache) & 15) ||
-      (reinterpret_cast<uintptr_t>(v_cache) & 15)) {
-    return fail(TI_EINVAL, "ti_gqa_prefill_paged: rows must be 16-byte aligned");
+      (reinterpret_cast<uintptr_t>(v_cache) & 15) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 255)) {
+    return fail(TI_EINVAL, "ti_gqa_prefill_paged: rows must be 16-byte aligned (workspace 256)");
   }
+  const bool bf16 = dtype == TI_DTYPE_BF16;
   PrefillArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.q_st = q_stride_t;
@@ -463,10 +918,40 @@ extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q
   a.page_size = page_size;
   a.max_blocks = max_blocks_per_seq;
   a.causal = causal ? 1 : 0;
+  a.tq = prefill_rows(head_dim) / a.group;
+  a.key_tile = 16 * kPrefillSubTiles;
   a.scale_log2 = float(1.4426950408889634 / sqrt(double(head_dim)));
+  a.balanced_wgs = 0;
+  a.max_pairs = 0;
+  a.min_chunk = kMinChunkTiles;
+  a.plan = nullptr;
+  a.part_o = nullptr;
+  a.part_ml = nullptr;
+  if (workspace != nullptr && workspace_bytes > 0) {
+    const int wgs = head_dim == 256 ? (bf16 ? balanced_wgs<256, Bf16>() : balanced_wgs<256, F16>())
+                                    : (bf16 ? balanced_wgs<128, Bf16>() : balanced_wgs<128, F16>());
+    int64_t pairs = 0, need = 0;
+    if (!balanced_sizes(batch, total_q, num_q_heads, num_kv_heads, head_dim, page_size,
+                        max_blocks_per_seq, wgs, &pairs, &need)) {
+      return fail(TI_EINVAL, "ti_gqa_prefill_paged: no balanced schedule for this call (batch %d); "
+                             "pass no workspace", batch);
+    }
+    if (workspace_bytes < need) {
+      return fail(TI_EINVAL, "ti_gqa_prefill_paged: workspace of %lld bytes needed, %lld given",
+                  (long long)need, (long long)workspace_bytes);
+    }
+    a.balanced_wgs = wgs;
+    a.max_pairs = int32_t(pairs);
+    a.plan = static_cast<int32_t*>(workspace);
+    const int64_t ints = (plan_ints(pairs, wgs) + 63) / 64 * 64;
+    a.part_o = reinterpret_cast<float*>(a.plan + ints);
+    a.part_ml = a.part_o + int64_t(wgs) * 2 * prefill_rows(head_dim) * head_dim;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool bf16 = dtype == TI_DTYPE_BF16;
-  if (head_dim == 256) launch_prefill<256, 1, 8, kPrefillSubTiles>(a, batch, max_seqlen_q, bf16, s);
-  else launch_prefill<128, 2, 8, kPrefillSubTiles>(a, batch, max_seqlen_q, bf16, s);
-  return check_launch("ti_gqa_prefill_paged");
+  if (head_dim == 256) {
+    return bf16 ? launch_prefill<256, Bf16>(a, batch, max_seqlen_q, s)
+                : launch_prefill<256, F16>(a, batch, max_seqlen_q, s);
+  }
+  return bf16 ? launch_prefill<128, Bf16>(a, batch, max_seqlen_q, s)
+              : launch_prefill<128, F16>(a, batch, max_seqlen_q, s);
 }

@@ -16,14 +16,33 @@ the causal mask is bottom-right aligned (query ``i`` sees keys ``j <= seqlen_k -
 query head ``h`` reads KV head ``h // (H_q // H_kv)``; softmax in base 2 with ``D^-1/2`` scale,
 P rounded to the cache dtype before P·V, fp32 accumulation; a row with no visible key is zero.
 The first chunk (no cached prefix) is the case ``seqlen_k == q_len``.
+
+Scheduling: by default every CU gets the same number of key tiles (a unit — one KV head of one
+block of query tokens — may be cut between workgroups and merged in fp32 afterwards, in a fixed
+order), so the causal triangle and ragged batches keep the whole GPU busy. ``batch_invariant=True``
+runs one workgroup per unit instead: each row's result is then bitwise independent of the other
+sequences in the batch and of how the prompt was chunked, at the cost of load balance.
 """
 from __future__ import annotations
+
+import ctypes
+import functools
 
 import torch
 
 from .. import _lib
 
 __all__ = ["gqa_prefill_paged_fn"]
+
+
+@functools.lru_cache(maxsize=256)
+def _workspace_bytes(batch: int, total_q: int, h_q: int, h_kv: int, d: int, page_size: int,
+                     width: int) -> int:
+    """Bytes of the balanced schedule's workspace (0: the call runs one workgroup per unit)."""
+    nbytes = ctypes.c_int64(0)
+    _lib.check(_lib.load().ti_gqa_prefill_workspace_bytes(batch, total_q, h_q, h_kv, d, page_size,
+                                                          width, ctypes.byref(nbytes)))
+    return nbytes.value
 
 
 def _aligned_rows(t: torch.Tensor) -> bool:
@@ -43,6 +62,7 @@ def gqa_prefill_paged_fn(
     *,
     causal: bool = True,
     out: torch.Tensor | None = None,
+    batch_invariant: bool = False,
 ) -> torch.Tensor:
     """Varlen (causal) GQA attention of packed queries over paged K/V.
 
@@ -58,6 +78,8 @@ def gqa_prefill_paged_fn(
         page_size: tokens per page of the flattened cache (a multiple of 16)
         causal: keyword-only; False drops the causal mask (the reference's ``is_causal=False``)
         out: keyword-only preallocated [total_q, H_q, D] output
+        batch_invariant: keyword-only; one workgroup per (sequence, KV head, query block)
+            instead of the balanced schedule (bitwise batch- and chunking-invariant rows)
     Returns:
         [total_q, H_q, D] tensor in q's dtype.
     """
@@ -122,10 +144,16 @@ def gqa_prefill_paged_fn(
         return out
     width = block_table.shape[1]
     lib = _lib.load()
+    ws, ws_bytes = None, 0
+    if not batch_invariant:
+        ws_bytes = _workspace_bytes(batch, total_q, h_q, h_kv, d, page_size, width)
+        if ws_bytes > 0:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     _lib.check(lib.ti_gqa_prefill_paged(
         q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
         block_table.data_ptr(), block_table.stride(0) if width > 0 else 0,
         cu_seqlens_q.data_ptr(), seqlen_k.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+        ws.data_ptr() if ws is not None else None, ws_bytes,
         batch, total_q, max_seqlen_q, h_q, h_kv, d, page_size, rows // page_size, width,
         1 if causal else 0, code, _lib.stream_handle(dev)))
     return out
