@@ -20,6 +20,7 @@ pages of ``page_size`` rows (kernels/gqa_decode_paged.py:403-406), so ``page_siz
 from __future__ import annotations
 
 import ctypes
+import functools
 
 import torch
 
@@ -31,6 +32,7 @@ _VARIANTS = {"auto": _lib.TI_DECODE_AUTO, "mfma": _lib.TI_DECODE_MFMA,
              "scalar": _lib.TI_DECODE_SCALAR}
 
 
+@functools.lru_cache(maxsize=256)
 def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
                 max_blocks_per_seq: int, split_tokens: int | None = None) -> tuple[int, int, int]:
     """(split_tokens, max_splits, workspace_bytes) the library uses for these host-known bounds."""
