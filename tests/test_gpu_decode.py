@@ -238,3 +238,26 @@ def test_graph_capture_replay(dev):
         eager = fn()
         torch.cuda.synchronize()
         assert torch.equal(bits(static_out), bits(eager)), f"replay {r}"
+
+
+@pytest.mark.parametrize("page", [32, 64])
+def test_larger_pages_vs_oracle(page, dev):
+    """Pages of 32 and 64 rows: the same cache rows addressed through coarser page ids."""
+    say(f"decode page_size={page}")
+    g = torch.Generator().manual_seed(page)
+    ctx = [5, page, page + 1, 3000]
+    need = sum((n + page - 1) // page for n in ctx)
+    perm = torch.randperm(need + 3, generator=g).to(torch.int32)
+    width = max((n + page - 1) // page for n in ctx)
+    table = torch.full((len(ctx), width), -1, dtype=torch.int32)
+    at = 0
+    for b, n in enumerate(ctx):
+        k = (n + page - 1) // page
+        table[b, :k] = perm[at:at + k]
+        at += k
+    kc = torch.randn(need + 3, page, 4, 256, generator=g).to(torch.bfloat16)
+    vc = torch.randn(need + 3, page, 4, 256, generator=g).to(torch.bfloat16)
+    q = torch.randn(len(ctx), 24, 256, generator=g).to(torch.bfloat16)
+    seq = torch.tensor(ctx, dtype=torch.int32)
+    out = gqa_decode_paged_fn(q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), seq.to(dev), page)
+    assert_decode_close(out, ref_gqa_decode_paged(q, kc, vc, table, seq, page))

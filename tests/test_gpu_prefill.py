@@ -234,3 +234,48 @@ def test_rejects_bad_arguments(dev):
     k96 = torch.zeros(kc.shape[0], 16, 4, 96, dtype=torch.bfloat16, device=dev)
     with pytest.raises(TileInferError):
         gqa_prefill_paged_fn(q96, k96, k96, bt, cu, sk)
+
+
+@pytest.mark.parametrize("invariant", MODES)
+def test_many_sequences_vs_oracle(invariant, dev):
+    """A ragged batch of 40 chunks (1 to 300 queries over up to 2,000 cached tokens, some empty):
+    hundreds of units, many of them cut between workgroups in the balanced schedule."""
+    say(f"prefill 40 ragged sequences invariant={invariant}")
+    g = torch.Generator().manual_seed(40)
+    q_lens = torch.randint(1, 301, (40,), generator=g).tolist()
+    q_lens[7] = 0
+    kv_lens = [q + int(torch.randint(0, 2001, (1,), generator=g)) for q in q_lens]
+    kv_lens[11] = 0                                  # no context at all: zero rows
+    step = prefill_step(q_lens, kv_lens, seed=41)
+    close(run_gpu(step, dev, batch_invariant=invariant), run_ref(step))
+
+
+def paged_step(q_lens, kv_lens, page, seed):
+    """A prefill step whose cache pages hold `page` rows (the flattened layout is the same)."""
+    g = torch.Generator().manual_seed(seed)
+    need = sum((n + page - 1) // page for n in kv_lens)
+    pool = need + 5
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    width = max((n + page - 1) // page for n in kv_lens)
+    table = torch.full((len(kv_lens), width), -1, dtype=torch.int32)
+    at = 0
+    for b, n in enumerate(kv_lens):
+        k = (n + page - 1) // page
+        table[b, :k] = perm[at:at + k]
+        at += k
+    kc = torch.randn(pool, page, 4, 256, generator=g).to(torch.bfloat16)
+    vc = torch.randn(pool, page, 4, 256, generator=g).to(torch.bfloat16)
+    cu = torch.tensor([0] + list(torch.tensor(q_lens).cumsum(0)), dtype=torch.int32)
+    q = torch.randn(int(cu[-1]), 24, 256, generator=g).to(torch.bfloat16)
+    return q, kc, vc, table, cu, torch.tensor(kv_lens, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("page", [32, 64])
+@pytest.mark.parametrize("invariant", MODES)
+def test_larger_pages_vs_oracle(page, invariant, dev):
+    """Pages of 32 and 64 rows (sub-tiles of 16 keys always lie inside one page)."""
+    say(f"prefill page_size={page} invariant={invariant}")
+    q, kc, vc, table, cu, sk = paged_step([50, 130], [700, 130], page, seed=page)
+    out = gqa_prefill_paged_fn(q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), cu.to(dev),
+                               sk.to(dev), 130, page, batch_invariant=invariant)
+    close(out, ref_gqa_prefill_paged(q, kc, vc, table, cu, sk, page))
