@@ -240,9 +240,9 @@ def test_graph_capture_replay(dev):
         assert torch.equal(bits(static_out), bits(eager)), f"replay {r}"
 
 
-@pytest.mark.parametrize("page", [32, 64])
+@pytest.mark.parametrize("page", [32, 48, 64])
 def test_larger_pages_vs_oracle(page, dev):
-    """Pages of 32 and 64 rows: the same cache rows addressed through coarser page ids."""
+    """Pages of 32, 48 and 64 rows: the same cache rows addressed through coarser page ids."""
     say(f"decode page_size={page}")
     g = torch.Generator().manual_seed(page)
     ctx = [5, page, page + 1, 3000]

@@ -270,10 +270,11 @@ def paged_step(q_lens, kv_lens, page, seed):
     return q, kc, vc, table, cu, torch.tensor(kv_lens, dtype=torch.int32)
 
 
-@pytest.mark.parametrize("page", [32, 64])
+@pytest.mark.parametrize("page", [32, 48, 64])
 @pytest.mark.parametrize("invariant", MODES)
 def test_larger_pages_vs_oracle(page, invariant, dev):
-    """Pages of 32 and 64 rows (sub-tiles of 16 keys always lie inside one page)."""
+    """Pages of 32, 48 (not a power of two: the division path) and 64 rows; sub-tiles of 16 keys
+    always lie inside one page."""
     say(f"prefill page_size={page} invariant={invariant}")
     q, kc, vc, table, cu, sk = paged_step([50, 130], [700, 130], page, seed=page)
     out = gqa_prefill_paged_fn(q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), cu.to(dev),

@@ -41,6 +41,7 @@ struct PrefillArgs {
   uint16_t* out;
   int64_t o_st, o_sh;
   int32_t total_q, num_blocks32, hq, hkv, group, page_size, max_blocks, causal;
+  int32_t page_shift;  // log2(page_size) when it is a power of two, else -1
   int32_t tq;        // query tokens per unit: floor(rows per workgroup / group)
   int32_t key_tile;  // keys per staged tile
   float scale_log2;
@@ -269,7 +270,9 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs 
 // stages in distinct arrays so that the compiler's wait counting tells the stage being loaded from
 // the stage being read. LDS rows are unpadded and swizzled (lds_swizzle) so that the MFMA operand
 // reads are free of bank conflicts.
-template <int D, int C, int W, int NS, typename Tag>
+// P2: page_size is a power of two (page_shift >= 0); pages are then found with shifts (a runtime
+// division costs ~20 scalar instructions, several per tile).
+template <int D, int C, int W, int NS, bool P2, typename Tag>
 __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int kKT = 16 * NS;
   constexpr int KK = D / 32;
@@ -325,6 +328,10 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   f32x4 o[C][NT];
   float m_run[C], l_run[C];
 
+  auto page_of = [&](int key) __attribute__((always_inline)) {
+    if constexpr (P2) return key >> a.page_shift;
+    else return key / a.page_size;
+  };
   // Block ids of the next tile to load (uniform), fetched one tile ahead of their use; -1 for a
   // sub-tile with nothing to load (past the context, or an absent page: masked, never loaded).
   int nbid[NS];
@@ -332,7 +339,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       const int key0 = k0 + 16 * j;
-      const int id = key0 < sx.kv_len ? bt_row[key0 / a.page_size] : -1;
+      const int id = key0 < sx.kv_len ? bt_row[page_of(key0)] : -1;
       nbid[j] = uint32_t(id) < uint32_t(a.num_blocks32) ? id : -1;
     }
   };
@@ -361,7 +368,8 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     const int rows = __builtin_amdgcn_readfirstlane(bid < 0 ? 0 : sub_rows(key0));
     bid = bid < 0 ? 0 : bid;
     const int64_t base = int64_t(bid) * a.page_stride +
-                         int64_t(key0 % a.page_size) * a.row_stride + int64_t(kvh) * D;
+                         int64_t(key0 - page_of(key0) * a.page_size) * a.row_stride +
+                         int64_t(kvh) * D;
     const uint32_t nbytes = rows > 0 ? uint32_t(rows - 1) * row_bytes + D * 2 : 0u;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k_cache + base, nbytes);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v_cache + base, nbytes);
@@ -764,7 +772,7 @@ int balanced_wgs() {
   static std::atomic<int> cached{0};  // same code object on every gfx950 device
   int per_cu = cached.load(std::memory_order_relaxed);
   if (per_cu == 0) {
-    const auto fn = prefill_mfma_kernel<D, S::C, S::W, kPrefillSubTiles, Tag>;
+    const auto fn = prefill_mfma_kernel<D, S::C, S::W, kPrefillSubTiles, true, Tag>;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
                                                      64 * S::W, 0) != hipSuccess || per_cu <= 0) {
       (void)hipGetLastError();
@@ -785,7 +793,8 @@ template <int D, typename Tag>
 int launch_prefill(const PrefillArgs& a0, int batch, int max_q, hipStream_t s) {
   using S = PrefillShape<D>;
   PrefillArgs a = a0;
-  const auto kern = prefill_mfma_kernel<D, S::C, S::W, kPrefillSubTiles, Tag>;
+  const auto kern = a.page_shift >= 0 ? prefill_mfma_kernel<D, S::C, S::W, kPrefillSubTiles, true, Tag>
+                                      : prefill_mfma_kernel<D, S::C, S::W, kPrefillSubTiles, false, Tag>;
   if (a.balanced_wgs == 0) {
     const dim3 grid(unsigned(a.hkv), unsigned(ceil_div(max_q, a.tq)), unsigned(batch));
     hipLaunchKernelGGL(kern, grid, dim3(64 * S::W), 0, s, a);
@@ -916,6 +925,7 @@ extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q
   a.hkv = num_kv_heads;
   a.group = num_q_heads / num_kv_heads;
   a.page_size = page_size;
+  a.page_shift = (page_size & (page_size - 1)) == 0 ? __builtin_ctz(unsigned(page_size)) : -1;
   a.max_blocks = max_blocks_per_seq;
   a.causal = causal ? 1 : 0;
   a.tq = prefill_rows(head_dim) / a.group;
