@@ -334,12 +334,16 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   };
   // Block ids of the next tile to load (uniform), fetched one tile ahead of their use; -1 for a
   // sub-tile with nothing to load (past the context, or an absent page: masked, never loaded).
+  // The ids are read with scalar loads: a vector load would be counted with the K/V loads into
+  // LDS, and waiting for the ids (used right away) would then wait for the whole tile in flight.
   int nbid[NS];
   auto load_ids = [&](int k0) __attribute__((always_inline)) {
+    typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+    const const_i32_ptr row = (const_i32_ptr)bt_row;
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       const int key0 = k0 + 16 * j;
-      const int id = key0 < sx.kv_len ? bt_row[page_of(key0)] : -1;
+      const int id = key0 < sx.kv_len ? row[page_of(key0)] : -1;
       nbid[j] = uint32_t(id) < uint32_t(a.num_blocks32) ? id : -1;
     }
   };
