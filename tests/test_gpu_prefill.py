@@ -32,7 +32,8 @@ def close(out, ref, atol=ATOL, rtol=RTOL):
     torch.testing.assert_close(out.float().cpu(), ref.float().cpu(), atol=atol, rtol=rtol)
 
 
-MODES = [pytest.param(False, id="balanced"), pytest.param(True, id="invariant")]
+MODES = [pytest.param(False, id="balanced"), pytest.param(True, id="per_unit")]
+SCHED = {False: "balanced", True: "per_unit"}
 
 
 @pytest.mark.parametrize("invariant", MODES)
@@ -48,7 +49,7 @@ MODES = [pytest.param(False, id="balanced"), pytest.param(True, id="invariant")]
 def test_vs_oracle(q_lens, kv_lens, invariant, dev):
     say(f"prefill q_lens={q_lens} kv_lens={kv_lens} invariant={invariant}")
     step = prefill_step(q_lens, kv_lens, seed=21)
-    out = run_gpu(step, dev, batch_invariant=invariant)
+    out = run_gpu(step, dev, schedule=SCHED[invariant])
     close(out, run_ref(step))
     exact = torch.from_numpy(prefill_fp64(
         step.q.double().numpy(), step.k_cache.double().numpy(), step.v_cache.double().numpy(),
@@ -60,7 +61,7 @@ def test_vs_oracle(q_lens, kv_lens, invariant, dev):
 def test_noncausal_vs_oracle(invariant, dev):
     say(f"prefill non-causal invariant={invariant}")
     step = prefill_step([40, 70], [90, 70], seed=22)
-    close(run_gpu(step, dev, causal=False, batch_invariant=invariant),
+    close(run_gpu(step, dev, causal=False, schedule=SCHED[invariant]),
           run_ref(step, causal=False))
 
 
@@ -71,7 +72,7 @@ def test_shapes_and_dtypes(hq, hkv, d, dtype, dev):
     say(f"prefill hq={hq} hkv={hkv} d={d} dtype={dtype}")
     step = prefill_step([70, 19], [1300, 19], seed=23, hq=hq, hkv=hkv, d=d, dtype=dtype)
     ref = run_ref(step)
-    close(run_gpu(step, dev), ref)
+    close(run_gpu(step, dev, schedule="balanced"), ref)
     close(run_gpu(step, dev, batch_invariant=True), ref)
 
 
@@ -80,8 +81,11 @@ def test_config4_first_chunk_vs_oracle(dev):
     step = config4_prefill()
     say("prefill config4 chunk 2048 (first chunk)")
     ref = run_ref(step)
-    close(run_gpu(step, dev), ref)
-    close(run_gpu(step, dev, batch_invariant=True), ref)
+    per_unit = run_gpu(step, dev, batch_invariant=True)
+    close(run_gpu(step, dev, schedule="balanced"), ref)
+    close(per_unit, ref)
+    # No cached context: the automatic choice is one workgroup per unit.
+    assert torch.equal(bits(run_gpu(step, dev, max_seqlen_k=2048)), bits(per_unit))
 
 
 def test_config4_continuation_schedules_agree(dev):
@@ -91,12 +95,15 @@ def test_config4_continuation_schedules_agree(dev):
     say("prefill config4 continuation: balanced vs invariant")
     st = config4_prefill(device=dev, cached=6144)
     args = (st.q, st.k_cache, st.v_cache, st.block_table, st.cu_seqlens_q, st.seqlen_k, 2048)
-    bal = gqa_prefill_paged_fn(*args)
+    bal = gqa_prefill_paged_fn(*args, schedule="balanced")
     inv = gqa_prefill_paged_fn(*args, batch_invariant=True)
     close(bal, inv, atol=1e-2, rtol=1e-2)
     same = (bits(bal) == bits(inv)).float().mean().item()
     assert same > 0.5, same                   # most rows come from uncut units: bitwise
-    assert torch.equal(bits(bal), bits(gqa_prefill_paged_fn(*args)))
+    assert torch.equal(bits(bal), bits(gqa_prefill_paged_fn(*args, schedule="balanced")))
+    # The automatic choice with the host bound the reference's context carries (max_seqlen_k):
+    # balanced here (cached context, uniform units: 392 of them for 256 CUs).
+    assert torch.equal(bits(bal), bits(gqa_prefill_paged_fn(*args, max_seqlen_k=8192)))
     # Spot rows against the oracle: query i alone over its visible keys 0..6144+i.
     rows = torch.arange(0, 2048, 97)
     ref = ref_gqa_prefill_paged(st.q[rows.to(dev)].cpu(), st.k_cache.cpu(), st.v_cache.cpu(),
@@ -161,8 +168,8 @@ def test_shared_prefix_equals_private_bitwise(invariant, dev):
         vc[private[1, j]] = vc[private[0, j]]
     args = (base.q.to(dev), kc.to(dev), vc.to(dev))
     tail = (base.cu_seqlens_q.to(dev), base.seqlen_k.to(dev), chunk)
-    a = gqa_prefill_paged_fn(*args, shared_bt.to(dev), *tail, batch_invariant=invariant)
-    b = gqa_prefill_paged_fn(*args, private.to(dev), *tail, batch_invariant=invariant)
+    a = gqa_prefill_paged_fn(*args, shared_bt.to(dev), *tail, schedule=SCHED[invariant])
+    b = gqa_prefill_paged_fn(*args, private.to(dev), *tail, schedule=SCHED[invariant])
     assert torch.equal(bits(a), bits(b))
 
 
@@ -187,7 +194,7 @@ def test_empty_contexts_give_zeros_and_rows_outside_untouched(invariant, dev):
     out = torch.full((q.shape[0], 24, 256), 7.0, dtype=torch.bfloat16, device=dev)
     gqa_prefill_paged_fn(q, step.k_cache.to(dev), step.v_cache.to(dev), step.block_table.to(dev),
                          step.cu_seqlens_q.to(dev), step.seqlen_k.to(dev), 6, out=out,
-                         batch_invariant=invariant)
+                         schedule=SCHED[invariant])
     o = out.float().cpu()
     assert (o[:4] == 0).all()                 # kv_len 0
     assert (o[4:7] == 0).all()                # offset -3: rows 0..2 see nothing
@@ -247,7 +254,7 @@ def test_many_sequences_vs_oracle(invariant, dev):
     kv_lens = [q + int(torch.randint(0, 2001, (1,), generator=g)) for q in q_lens]
     kv_lens[11] = 0                                  # no context at all: zero rows
     step = prefill_step(q_lens, kv_lens, seed=41)
-    close(run_gpu(step, dev, batch_invariant=invariant), run_ref(step))
+    close(run_gpu(step, dev, schedule=SCHED[invariant]), run_ref(step))
 
 
 def paged_step(q_lens, kv_lens, page, seed):
@@ -278,5 +285,23 @@ def test_larger_pages_vs_oracle(page, invariant, dev):
     say(f"prefill page_size={page} invariant={invariant}")
     q, kc, vc, table, cu, sk = paged_step([50, 130], [700, 130], page, seed=page)
     out = gqa_prefill_paged_fn(q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), cu.to(dev),
-                               sk.to(dev), 130, page, batch_invariant=invariant)
+                               sk.to(dev), 130, page, schedule=SCHED[invariant])
     close(out, ref_gqa_prefill_paged(q, kc, vc, table, cu, sk, page))
+
+
+@pytest.mark.parametrize("invariant", MODES)
+def test_repeated_calls_bitwise_identical(invariant, dev):
+    """Every K/V stage is loaded into LDS by all waves together; each must wait for its own loads
+    before the barrier that publishes the stage. Without that wait a wave could read another
+    wave's part before it landed and a few calls in a hundred came out different: 24 repeats of
+    the ragged 40-sequence batch must agree bitwise."""
+    say(f"prefill repeated calls invariant={invariant}")
+    g = torch.Generator().manual_seed(40)
+    q_lens = torch.randint(1, 301, (40,), generator=g).tolist()
+    kv_lens = [q + int(torch.randint(0, 2001, (1,), generator=g)) for q in q_lens]
+    step = prefill_step(q_lens, kv_lens, seed=41)
+    args = (step.q.to(dev), step.k_cache.to(dev), step.v_cache.to(dev), step.block_table.to(dev),
+            step.cu_seqlens_q.to(dev), step.seqlen_k.to(dev), step.max_seqlen_q)
+    first = bits(gqa_prefill_paged_fn(*args, schedule=SCHED[invariant]))
+    for _ in range(23):
+        assert torch.equal(bits(gqa_prefill_paged_fn(*args, schedule=SCHED[invariant])), first)

@@ -547,17 +547,22 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       fetch(sk0, sv0, empty_st[0], t0 * kKT);
       if (cnt > 1) load_ids((t0 + 1) * kKT);
     }
-    // Two tiles per trip so that each stage is a compile-time array.
+    // Two tiles per trip so that each stage is a compile-time array. Each wave loads only part of
+    // a stage, so before the barrier every wave must wait for its own K/V loads into LDS to land
+    // (vmcnt): the compiler's __syncthreads does not count those loads as writes to order, and
+    // its per-wave waits before the LDS reads cover only the reading wave's own part.
     for (int it = 0; it < cnt; it += 2) {
       const int k0 = (t0 + it) * kKT;
-      __syncthreads();  // stage 0 holds tile it; every wave is done with stage 1
+      // Stage 0 holds tile it; every wave is done with stage 1.
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if (it + 1 < cnt) {
         fetch(sk1, sv1, empty_st[1], k0 + kKT);
         if (it + 2 < cnt) load_ids(k0 + 2 * kKT);
       }
       if (k0 <= wave_last_key) compute(sk0, sv0, empty_st[0], k0);
       if (it + 1 >= cnt) break;
-      __syncthreads();  // stage 1 holds tile it + 1; every wave is done with stage 0
+      // Stage 1 holds tile it + 1; every wave is done with stage 0.
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if (it + 2 < cnt) {
         fetch(sk0, sv0, empty_st[0], k0 + 2 * kKT);
         if (it + 3 < cnt) load_ids(k0 + 3 * kKT);

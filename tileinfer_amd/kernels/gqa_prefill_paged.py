@@ -17,16 +17,22 @@ query head ``h`` reads KV head ``h // (H_q // H_kv)``; softmax in base 2 with ``
 P rounded to the cache dtype before P·V, fp32 accumulation; a row with no visible key is zero.
 The first chunk (no cached prefix) is the case ``seqlen_k == q_len``.
 
-Scheduling: by default every CU gets the same number of key tiles (a unit — one KV head of one
-block of query tokens — may be cut between workgroups and merged in fp32 afterwards, in a fixed
-order), so the causal triangle and ragged batches keep the whole GPU busy. ``batch_invariant=True``
-runs one workgroup per unit instead: each row's result is then bitwise independent of the other
-sequences in the batch and of how the prompt was chunked, at the cost of load balance.
+Scheduling. A unit is one KV head of one block of query tokens. ``schedule="per_unit"`` runs one
+workgroup per unit (one launch, heaviest blocks first): each row's result is then bitwise
+independent of the other sequences in the batch and of how the prompt was chunked
+(``batch_invariant=True`` asks for exactly that). ``schedule="balanced"`` gives every CU the same
+work (units may be cut between workgroups and merged in fp32 afterwards, in a fixed order; three
+launches), which removes the partial last round of a continuation chunk and spreads a few long
+units over the whole GPU. ``schedule="auto"`` (default) picks per call from host-known sizes: the
+per-unit schedule when no sequence has cached context (``max_seqlen_k <= max_seqlen_q``: causal
+first chunks pack well heaviest-first), a greedy estimate of both for a single sequence, the
+balanced schedule otherwise (and whenever ``max_seqlen_k`` is not given).
 """
 from __future__ import annotations
 
 import ctypes
 import functools
+import heapq
 
 import torch
 
@@ -43,6 +49,46 @@ def _workspace_bytes(batch: int, total_q: int, h_q: int, h_kv: int, d: int, page
     _lib.check(_lib.load().ti_gqa_prefill_workspace_bytes(batch, total_q, h_q, h_kv, d, page_size,
                                                           width, ctypes.byref(nbytes)))
     return nbytes.value
+
+
+# Schedule model (in 64-key tiles): a unit costs its key tiles plus _UNIT_COST (start-up and
+# epilogue); the balanced schedule adds its plan and merge launches, ~_BALANCE_OVERHEAD tiles.
+_KEY_TILE, _UNIT_COST, _BALANCE_OVERHEAD = 64, 2, 9
+
+
+@functools.lru_cache(maxsize=1024)
+def _per_unit_wins(q_len: int, kv_len: int, causal: bool, h_kv: int, tq: int, wgs: int) -> bool:
+    """One sequence: greedy (heaviest-first) makespan of one workgroup per unit against the
+    balanced schedule's even share plus its overhead."""
+    costs = []
+    for qb0 in range(0, q_len, tq):
+        t = min(tq, q_len - qb0)
+        k_end = min(kv_len, kv_len - q_len + qb0 + t) if causal else kv_len
+        nt = -(-max(k_end, 0) // _KEY_TILE)
+        if nt:
+            costs.extend([nt + _UNIT_COST] * h_kv)
+    if not costs:
+        return True
+    costs.sort(reverse=True)
+    loads = [0] * min(wgs, len(costs))
+    heapq.heapify(loads)
+    for c in costs:
+        heapq.heappush(loads, heapq.heappop(loads) + c)
+    return max(loads) <= sum(costs) / wgs + _BALANCE_OVERHEAD
+
+
+def _choose_per_unit(batch: int, total_q: int, max_q: int, max_k: int | None, causal: bool,
+                     h_q: int, h_kv: int, d: int, dev: torch.device) -> bool:
+    if max_k is None:
+        return False
+    if causal and max_k <= max_q:
+        return True  # no cached context: first chunks
+    if batch != 1:
+        return False
+    rows = 128 if d == 256 else 256           # rows of a workgroup (the kernel's launch shape)
+    tq = rows // (h_q // h_kv)
+    wgs = torch.cuda.get_device_properties(dev).multi_processor_count
+    return _per_unit_wins(int(total_q), int(max_k), bool(causal), h_kv, tq, wgs)
 
 
 def _aligned_rows(t: torch.Tensor) -> bool:
@@ -63,6 +109,8 @@ def gqa_prefill_paged_fn(
     causal: bool = True,
     out: torch.Tensor | None = None,
     batch_invariant: bool = False,
+    max_seqlen_k: int | None = None,
+    schedule: str = "auto",
 ) -> torch.Tensor:
     """Varlen (causal) GQA attention of packed queries over paged K/V.
 
@@ -78,8 +126,11 @@ def gqa_prefill_paged_fn(
         page_size: tokens per page of the flattened cache (a multiple of 16)
         causal: keyword-only; False drops the causal mask (the reference's ``is_causal=False``)
         out: keyword-only preallocated [total_q, H_q, D] output
-        batch_invariant: keyword-only; one workgroup per (sequence, KV head, query block)
-            instead of the balanced schedule (bitwise batch- and chunking-invariant rows)
+        batch_invariant: keyword-only; forces the per-unit schedule (bitwise batch- and
+            chunking-invariant rows)
+        max_seqlen_k: keyword-only host bound on every ``seqlen_k`` (the reference's
+            ``ctx.max_seqlen_k``); only used to choose the schedule
+        schedule: keyword-only, "auto", "balanced" or "per_unit" (see the module docstring)
     Returns:
         [total_q, H_q, D] tensor in q's dtype.
     """
@@ -144,8 +195,13 @@ def gqa_prefill_paged_fn(
         return out
     width = block_table.shape[1]
     lib = _lib.load()
+    if schedule not in ("auto", "balanced", "per_unit"):
+        raise ValueError(f"schedule must be 'auto', 'balanced' or 'per_unit', got {schedule!r}")
+    per_unit = batch_invariant or schedule == "per_unit" or (
+        schedule == "auto" and _choose_per_unit(batch, total_q, max_seqlen_q, max_seqlen_k, causal,
+                                                h_q, h_kv, d, dev))
     ws, ws_bytes = None, 0
-    if not batch_invariant:
+    if not per_unit:
         ws_bytes = _workspace_bytes(batch, total_q, h_q, h_kv, d, page_size, width)
         if ws_bytes > 0:
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
