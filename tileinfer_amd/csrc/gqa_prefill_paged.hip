@@ -60,9 +60,6 @@ constexpr int kMinChunkTiles = 4;     // shortest run of key tiles of a balanced
 constexpr int kXcds = 8;              // MI355X: 8 XCDs of 32 CUs, one L2 each
 constexpr int kUnitCost = 2;          // a unit's start-up and epilogue, priced in key tiles
 static_assert(kMinChunkTiles > kUnitCost, "every balanced run must reach a key tile");
-// Instruction classes of __builtin_amdgcn_sched_group_barrier.
-constexpr int kSchedMfma = 0x008;
-constexpr int kSchedDsRead = 0x100;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
