@@ -3,7 +3,8 @@
 // Replaces tileInfer's chunked-prefill attention, which first gathers every cached position of the
 // sequence through the block table into contiguous K/V copies (model/qwen_36.py:1030-1044) and then
 // runs varlen flash attention on them (kernels/gqa_varlen.py:40-185, dispatch 369-389). Here the
-// cache pages are the operand: no gather copy, one launch for any number of sequences.
+// cache pages are the operand: no gather copy, any number of sequences per call (one launch per
+// unit schedule; schedule + attention + merge launches for the balanced one, see below).
 //
 // Semantics (kernels/gqa_varlen.py:88-131, 144-175): sequence b has q_len = cu_q[b+1] - cu_q[b]
 // query tokens and kv_len = seqlen_k[b] cached tokens (the chunk's own K/V already appended); the
@@ -13,8 +14,9 @@
 // sees all kv_len keys), the reference's is_causal=False. As in the decode kernel, a block id
 // outside [0, num_blocks) inside the context is an absent page: its keys are masked, never loaded.
 //
-// Work unit: a workgroup = one (sequence, KV head, block of query tokens), whose rows are the
-// (token, query head) pairs of the KV head's group, so each 64-key K/V tile staged in LDS is shared
+// Work unit: (sequence, KV head, block of query tokens), whose rows are the (token, query head)
+// pairs of the KV head's group; a workgroup computes one unit (or, balanced, a run of key tiles
+// over consecutive units), so each 64-key K/V tile staged in LDS is shared
 // by every query head of the group (GQA packing) and each K/V operand read from LDS feeds C MFMAs
 // (C column tiles of 16 rows per wave). Tiles are loaded straight from the pages one tile ahead,
 // through per-page buffer descriptors. Each wave uses the transposed MFMA layout:
