@@ -16,6 +16,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--varia
 from __future__ import annotations
 
 import argparse
+import functools
 import json
 import os
 import re
@@ -189,6 +190,20 @@ def _time(fn, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) * 1e3 / steps
 
 
+def _time_interleaved(fns, steps: int, warmup: int, rounds: int = 5) -> list:
+    """Median over `rounds` of the mean µs of each fn over `steps` calls, the functions taking
+    turns in every round (so clock ramps and a neighbour's state weigh on all of them alike)."""
+    for fn in fns:
+        for _ in range(warmup):
+            fn()
+    torch.cuda.synchronize()
+    per_fn = [[] for _ in fns]
+    for _ in range(rounds):
+        for i, fn in enumerate(fns):
+            per_fn[i].append(_time(fn, steps, 0))
+    return [statistics.median(v) for v in per_fn]
+
+
 def swap_config5(st, dev, args, layers: int = 16, fraction: float = 0.25) -> dict:
     """Config 5's swap: a quarter of the sequences' unique blocks, K and V of all 16 layers, to
     pinned host memory and back into fresh block ids, through one block-list launch each way."""
@@ -359,18 +374,16 @@ def prefill_config4(st, chunk_slots, kc, vc, dev, args) -> dict:
     # The default ("auto") schedule chooses from host sizes, here with the max_seqlen_k the
     # reference's context carries; both schedules are also timed on their own.
     scheds = ("auto", "balanced", "per_unit")
-    first_us, first_bal_us, first_pu_us = (
-        _time(lambda: gqa_prefill_paged_fn(q, kc, vc, table, cu, sk, chunk, schedule=sc,
-                                           max_seqlen_k=chunk), args.steps, args.warmup)
-        for sc in scheds)
+    first_us, first_bal_us, first_pu_us = _time_interleaved(
+        [functools.partial(gqa_prefill_paged_fn, q, kc, vc, table, cu, sk, chunk, schedule=sc,
+                           max_seqlen_k=chunk) for sc in scheds], args.steps, args.warmup)
     first_flops = wl.prefill_flops([chunk], [chunk])
     cont = wl.config4_prefill(device=dev, cached=6144, chunk=chunk)
     kv_len = int(cont.seqlen_k[0])
-    cont_us, cont_bal_us, cont_pu_us = (
-        _time(lambda: gqa_prefill_paged_fn(cont.q, cont.k_cache, cont.v_cache, cont.block_table,
-                                           cont.cu_seqlens_q, cont.seqlen_k, chunk, schedule=sc,
-                                           max_seqlen_k=kv_len), args.steps, args.warmup)
-        for sc in scheds)
+    cont_us, cont_bal_us, cont_pu_us = _time_interleaved(
+        [functools.partial(gqa_prefill_paged_fn, cont.q, cont.k_cache, cont.v_cache,
+                           cont.block_table, cont.cu_seqlens_q, cont.seqlen_k, chunk, schedule=sc,
+                           max_seqlen_k=kv_len) for sc in scheds], args.steps, args.warmup)
     cont_flops = cont.flops()
     pos = torch.arange(kv_len, device=dev)
     blocks = cont.block_table[0, pos // BLOCK].long()

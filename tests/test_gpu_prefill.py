@@ -89,20 +89,18 @@ def test_config4_first_chunk_vs_oracle(dev):
 
 
 def test_config4_continuation_schedules_agree(dev):
-    """Config 4's continuation chunk (2048 queries over 8192 keys, 392 units on 256 CUs): the
-    balanced schedule against the one-unit-per-workgroup one (same arithmetic per key tile; cut
-    units merged in fp32, so equal within rounding), and the balanced run is deterministic."""
+    """Config 4's continuation chunk (2048 queries over 8192 keys): the balanced schedule (192-row
+    units, 32-key tiles, cut units merged in fp32) against the one-unit-per-workgroup one (128-row
+    units, 64-key tiles): equal within rounding; the balanced run is deterministic."""
     say("prefill config4 continuation: balanced vs invariant")
     st = config4_prefill(device=dev, cached=6144)
     args = (st.q, st.k_cache, st.v_cache, st.block_table, st.cu_seqlens_q, st.seqlen_k, 2048)
     bal = gqa_prefill_paged_fn(*args, schedule="balanced")
     inv = gqa_prefill_paged_fn(*args, batch_invariant=True)
     close(bal, inv, atol=1e-2, rtol=1e-2)
-    same = (bits(bal) == bits(inv)).float().mean().item()
-    assert same > 0.5, same                   # most rows come from uncut units: bitwise
     assert torch.equal(bits(bal), bits(gqa_prefill_paged_fn(*args, schedule="balanced")))
     # The automatic choice with the host bound the reference's context carries (max_seqlen_k):
-    # balanced here (cached context, uniform units: 392 of them for 256 CUs).
+    # balanced here (cached context, 256 units of 192 rows, one per CU but cut in merged runs).
     assert torch.equal(bits(bal), bits(gqa_prefill_paged_fn(*args, max_seqlen_k=8192)))
     # Spot rows against the oracle: query i alone over its visible keys 0..6144+i.
     rows = torch.arange(0, 2048, 97)

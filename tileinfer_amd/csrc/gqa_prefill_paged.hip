@@ -16,7 +16,7 @@
 //
 // Work unit: (sequence, KV head, block of query tokens), whose rows are the (token, query head)
 // pairs of the KV head's group; a workgroup computes one unit (or, balanced, a run of key tiles
-// over consecutive units), so each 64-key K/V tile staged in LDS is shared
+// over consecutive units), so each K/V tile staged in LDS (32 or 64 keys) is shared
 // by every query head of the group (GQA packing) and each K/V operand read from LDS feeds C MFMAs
 // (C column tiles of 16 rows per wave). Tiles are loaded straight from the pages one tile ahead,
 // through per-page buffer descriptors. Each wave uses the transposed MFMA layout:
@@ -54,9 +54,6 @@ struct PrefillArgs {
   float* part_ml;  // [balanced_wgs][2][rows][2] their (m, l), m in exp2 units
 };
 
-// A staged tile holds NS 16-key sub-tiles (each inside one page): kKT = 16 * NS keys. Four
-// (64 keys) measured 1-3 % faster than two in a same-process A/B on MI355X.
-constexpr int kPrefillSubTiles = 4;
 constexpr float kRescaleSlack = 8.f;  // exp2 units a row maximum may rise before O is rescaled
 constexpr int kMinChunkTiles = 4;     // shortest run of key tiles of a balanced workgroup
 constexpr int kXcds = 8;              // MI355X: 8 XCDs of 32 CUs, one L2 each
@@ -278,9 +275,14 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int NT = D / 16;
   constexpr int CPR = D / 8;              // 16-byte chunks per row
   constexpr int RPB = 1024 / (2 * D);     // rows per 1 KiB load (64 lanes x 16 bytes)
-  constexpr int LPW = kKT / RPB / W;      // 1 KiB loads per wave per tile, each of K and V
+  constexpr int LW = W < 8 ? W : 8;       // waves that load the tiles (the others only compute)
+  constexpr int LPW = kKT / RPB / LW;     // 1 KiB loads per loading wave per tile, each of K and V
   constexpr int ROWS = 16 * C * W;        // rows of the workgroup
-  static_assert(LPW * RPB * W == kKT && 16 % (kKT / W) == 0,
+  // Register-lean forms for shapes above 8 waves (3 waves per SIMD leave 168 VGPRs): V offsets
+  // computed per read, K operands read through a ring, load offsets recomputed per tile. Each
+  // costs the 8-wave shape 1-3 % (same-process A/B), which therefore keeps the plain forms.
+  constexpr bool kLean = W > 8;
+  static_assert(LPW * RPB * LW == kKT && 16 % (kKT / LW) == 0,
                 "each wave's loads must lie inside one sub-tile");
 
   __shared__ __align__(1024) uint16_t sk0[kKT * D];
@@ -301,20 +303,28 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   // of the A operand (keys 4g + i of sub-tile h, matching P). voff[h][dt % 8] is the element
   // offset inside a stage of d-tile dt's piece; d-tiles dt and dt + 8 differ by 128 elements
   // (the swizzle only permutes chunks inside each group of 16).
-  int voff[2][8];
+  // Lean form: the swizzle XORs the 16-byte chunk index 2 dl + ((s % 4) / 2) with the even
+  // 2r & 14, i.e. element offset 16 (dl ^ (r & 7)) + 8 ((s % 4) / 2), so voff[h][dl] =
+  // vbase[h] + (16 dl ^ vxor[h]): one v_xad per read instead of 16 live offsets.
+  int voff[2][kLean ? 1 : 8];
+  int vbase[2], vxor[2];
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
     const int r = 16 * hh + 4 * g + (n >> 2);
-    const int sw = lds_swizzle_v(r);
+    vbase[hh] = r * D + ((n & 3) >> 1) * 8 + (n & 1) * 4;
+    vxor[hh] = 16 * (r & 7);
+    if constexpr (!kLean) {
+      const int sw = lds_swizzle_v(r);
 #pragma unroll
-    for (int dl = 0; dl < 8; ++dl) {
-      const int y = 2 * dl + ((n & 3) >> 1);
-      voff[hh][dl] = r * D + ((y ^ sw) * 8) + (n & 1) * 4;
+      for (int dl = 0; dl < 8; ++dl) {
+        const int y = 2 * dl + ((n & 3) >> 1);
+        voff[hh][dl] = r * D + ((y ^ sw) * 8) + (n & 1) * 4;
+      }
     }
   }
   const uint32_t row_bytes = uint32_t(a.row_stride) * 2u;
   // The sub-tile this wave loads (kKT / W rows per wave, inside one sub-tile).
-  const int my_sub = (wave * (kKT / W)) / 16;
+  const int my_sub = (min(wave, LW - 1) * (kKT / LW)) / 16;
 
   // The current unit (uniform) and this lane's C rows of it.
   int b = 0, kvh = 0, qb0 = 0;
@@ -376,11 +386,17 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     const uint32_t nbytes = rows > 0 ? uint32_t(rows - 1) * row_bytes + D * 2 : 0u;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k_cache + base, nbytes);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v_cache + base, nbytes);
+    if (wave >= LW) return;  // uniform
+    // Lean form: the per-lane offsets are recomputed at every fetch (an opaque copy of the lane
+    // index keeps the compiler from hoisting 2 * LPW of them out of the loop, where they would
+    // be spilled).
+    int ln = lane;
+    if constexpr (kLean) asm volatile("" : "+v"(ln));
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int blk = wave * LPW + i;                  // 1 KiB block of the tile (uniform)
-      const int row = blk * RPB + lane / CPR;          // tile row of this lane's chunk
-      const int slot = lane % CPR;
+      const int row = blk * RPB + ln / CPR;            // tile row of this lane's chunk
+      const int slot = ln % CPR;
       const int chunk_k = slot ^ lds_swizzle(row);
       const int chunk_v = slot ^ lds_swizzle_v(row);
       const uint32_t off_k = uint32_t(row & 15) * row_bytes + uint32_t(chunk_k) * 16u;
@@ -402,16 +418,34 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       rows[j] = 0;
       if (k0 + 16 * j <= wave_last_key) {  // uniform
         rows[j] = ((empty >> j) & 1u) ? 0 : sub_rows(k0 + 16 * j);
-        u32x4 kop[KK];
+        auto read_k = [&](int kk) __attribute__((always_inline)) {
+          return *reinterpret_cast<const u32x4*>(sk + (16 * j + n) * D +
+                                                (((4 * kk + g) ^ lds_swizzle(n)) * 8));
+        };
+        if constexpr (kLean) {
+          // K reads two k-steps ahead of their MFMAs (a ring of three operands).
+          u32x4 kop[3];
+          kop[0] = read_k(0);
+          kop[1] = read_k(1);
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          kop[kk] = *reinterpret_cast<const u32x4*>(
-              sk + (16 * j + n) * D + (((4 * kk + g) ^ lds_swizzle(n)) * 8));
-        }
+          for (int kk = 0; kk < KK; ++kk) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (kk + 2 < KK) kop[(kk + 2) % 3] = read_k(kk + 2);
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
+            for (int c = 0; c < C; ++c) {
+              s[j][c] = mfma16x16x32(kop[kk % 3], qop[c][kk], s[j][c], Tag{});
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          u32x4 kop[KK];
 #pragma unroll
-          for (int c = 0; c < C; ++c) s[j][c] = mfma16x16x32(kop[kk], qop[c][kk], s[j][c], Tag{});
+          for (int kk = 0; kk < KK; ++kk) kop[kk] = read_k(kk);
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+            for (int c = 0; c < C; ++c) s[j][c] = mfma16x16x32(kop[kk], qop[c][kk], s[j][c], Tag{});
+          }
         }
       }
     }
@@ -485,8 +519,16 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       const uint16_t* svh = sv + 32 * h * D;
       auto read_v = [&](int dt) __attribute__((always_inline)) {
         const int dh = dt >> 3, dl = dt & 7;
-        const u32x2 lo = lds_read_tr4(svh + voff[0][dl] + 128 * dh);
-        const u32x2 hi = lds_read_tr4(svh + voff[1][dl] + 128 * dh);
+        int o0, o1;
+        if constexpr (kLean) {
+          o0 = vbase[0] + ((16 * dl) ^ vxor[0]);
+          o1 = vbase[1] + ((16 * dl) ^ vxor[1]);
+        } else {
+          o0 = voff[0][dl];
+          o1 = voff[1][dl];
+        }
+        const u32x2 lo = lds_read_tr4(svh + o0 + 128 * dh);
+        const u32x2 hi = lds_read_tr4(svh + o1 + 128 * dh);
         return u32x4{lo[0], lo[1], hi[0], hi[1]};
       };
       u32x4 vop[3];
@@ -766,23 +808,43 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
   }
 }
 
-// Launch shape per head_dim: C column tiles per wave, W waves.
-template <int D> struct PrefillShape;
-template <> struct PrefillShape<256> { static constexpr int C = 1, W = 8; };
-template <> struct PrefillShape<128> { static constexpr int C = 2, W = 8; };
+// Launch shape per head_dim and schedule: C column tiles per wave, W waves (16 C W rows), NS
+// 16-key sub-tiles per staged tile (each inside one page). head_dim 256, measured in same-process
+// A/Bs on MI355X (config 4, 6 query heads per KV head):
+// - one workgroup per unit: 8 waves, 64-key tiles. Units of 128 rows keep a causal first chunk's
+//   longest unit short (82 us for the 2048-token chunk; 12 waves x 192 rows: 106-115 us).
+// - balanced: 12 waves (3 per SIMD, 168 VGPRs), 32-key tiles. 192 rows share each K/V tile, 1.5x
+//   the rows of 8 waves, and the 32-key tile leaves the registers the third wave needs (64-key
+//   tiles spill 22 VGPRs): continuation chunk 405 us against 444 us for 8 waves.
+template <int D, bool BAL> struct PrefillShape;
+template <> struct PrefillShape<256, false> { static constexpr int C = 1, W = 8, NS = 4; };
+template <> struct PrefillShape<256, true> { static constexpr int C = 1, W = 12, NS = 2; };
+template <bool BAL> struct PrefillShape<128, BAL> { static constexpr int C = 2, W = 8, NS = 4; };
 
-int prefill_rows(int head_dim) { return head_dim == 256 ? 16 * 1 * 8 : 16 * 2 * 8; }
+int prefill_rows(int head_dim, bool balanced) {
+  return head_dim == 256 ? (balanced ? 16 * 1 * 12 : 16 * 1 * 8) : 16 * 2 * 8;
+}
+int prefill_key_tile(int head_dim, bool balanced) {
+  return head_dim == 256 && balanced ? 16 * 2 : 16 * 4;
+}
+
+template <int D, bool BAL, bool P2, typename Tag>
+constexpr auto prefill_kernel() {
+  using S = PrefillShape<D, BAL>;
+  return prefill_mfma_kernel<D, S::C, S::W, S::NS, P2, Tag>;
+}
 
 // Workgroups of one balanced launch: every CU's resident workgroups (one round).
 template <int D, typename Tag>
 int balanced_wgs() {
-  using S = PrefillShape<D>;
   static std::atomic<int> cached{0};  // same code object on every gfx950 device
   int per_cu = cached.load(std::memory_order_relaxed);
   if (per_cu == 0) {
-    const auto fn = prefill_mfma_kernel<D, S::C, S::W, kPrefillSubTiles, true, Tag>;
+    const auto fn = prefill_kernel<D, true, true, Tag>();
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
-                                                     64 * S::W, 0) != hipSuccess || per_cu <= 0) {
+                                                     64 * PrefillShape<D, true>::W, 0) !=
+            hipSuccess ||
+        per_cu <= 0) {
       (void)hipGetLastError();
       per_cu = 1;
     }
@@ -793,34 +855,34 @@ int balanced_wgs() {
 
 // Upper bound of balanced_wgs (LDS bounds the resident workgroups per CU).
 int balanced_wgs_bound(int head_dim) {
-  const int lds = 4 * 16 * kPrefillSubTiles * head_dim * 2;
+  const int lds = 4 * prefill_key_tile(head_dim, true) * head_dim * 2;
   return device_cu_count() * (160 * 1024 / lds);
 }
 
-template <int D, typename Tag>
-int launch_prefill(const PrefillArgs& a0, int batch, int max_q, hipStream_t s) {
-  using S = PrefillShape<D>;
-  PrefillArgs a = a0;
-  const auto kern = a.page_shift >= 0 ? prefill_mfma_kernel<D, S::C, S::W, kPrefillSubTiles, true, Tag>
-                                      : prefill_mfma_kernel<D, S::C, S::W, kPrefillSubTiles, false, Tag>;
-  if (a.balanced_wgs == 0) {
+template <int D, bool BAL, typename Tag>
+int launch_prefill(const PrefillArgs& a, int batch, int max_q, hipStream_t s) {
+  using S = PrefillShape<D, BAL>;
+  const auto kern = a.page_shift >= 0 ? prefill_kernel<D, BAL, true, Tag>()
+                                      : prefill_kernel<D, BAL, false, Tag>();
+  if constexpr (!BAL) {
     const dim3 grid(unsigned(a.hkv), unsigned(ceil_div(max_q, a.tq)), unsigned(batch));
     hipLaunchKernelGGL(kern, grid, dim3(64 * S::W), 0, s, a);
     return check_launch("ti_gqa_prefill_paged");
+  } else {
+    hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, a, batch);
+    int rc = check_launch("ti_gqa_prefill_paged (plan)");
+    if (rc != TI_OK) return rc;
+    hipLaunchKernelGGL(kern, dim3(unsigned(a.balanced_wgs)), dim3(64 * S::W), 0, s, a);
+    rc = check_launch("ti_gqa_prefill_paged");
+    if (rc != TI_OK) return rc;
+    constexpr int kRows = 16 * S::C * S::W;
+    constexpr int kMergeRows = 256 / (D / 8) * kMergeRowsPerThread;  // rows per merge workgroup
+    static_assert(kRows % kMergeRows == 0, "merge row blocks must tile the unit");
+    hipLaunchKernelGGL((prefill_merge_kernel<D, kRows, Tag>),
+                       dim3(unsigned(a.max_pairs), unsigned(a.hkv), unsigned(kRows / kMergeRows)),
+                       dim3(256), 0, s, a);
+    return check_launch("ti_gqa_prefill_paged (merge)");
   }
-  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, a, batch);
-  int rc = check_launch("ti_gqa_prefill_paged (plan)");
-  if (rc != TI_OK) return rc;
-  hipLaunchKernelGGL(kern, dim3(unsigned(a.balanced_wgs)), dim3(64 * S::W), 0, s, a);
-  rc = check_launch("ti_gqa_prefill_paged");
-  if (rc != TI_OK) return rc;
-  constexpr int kRows = 16 * S::C * S::W;
-  constexpr int kMergeRows = 256 / (D / 8) * kMergeRowsPerThread;  // rows per merge workgroup
-  static_assert(kRows % kMergeRows == 0, "merge row blocks must tile the unit");
-  hipLaunchKernelGGL((prefill_merge_kernel<D, kRows, Tag>),
-                     dim3(unsigned(a.max_pairs), unsigned(a.hkv), unsigned(kRows / kMergeRows)),
-                     dim3(256), 0, s, a);
-  return check_launch("ti_gqa_prefill_paged (merge)");
 }
 
 // Balanced-schedule sizes of one call; false when the call runs one workgroup per unit (too many
@@ -829,17 +891,17 @@ bool balanced_sizes(int32_t batch, int32_t total_q, int32_t hq, int32_t hkv, int
                     int32_t page_size, int32_t max_blocks, int64_t wgs, int64_t* max_pairs,
                     int64_t* bytes) {
   if (batch <= 0 || batch > kMaxPlanSeqs || hkv <= 0 || hq % hkv != 0) return false;
-  const int64_t tq = prefill_rows(head_dim) / (hq / hkv);
+  const int64_t tq = prefill_rows(head_dim, true) / (hq / hkv);
   if (tq <= 0) return false;
   const int64_t pairs = ceil_div(total_q, tq) + batch;
-  const int64_t kt = 16 * kPrefillSubTiles;
+  const int64_t kt = prefill_key_tile(head_dim, true);
   const int64_t tiles_bound =
       pairs * (ceil_div(int64_t(max_blocks) * page_size, kt) + kUnitCost) * hkv;
   if (pairs > INT32_MAX / 8 || tiles_bound > INT32_MAX / 2 || hkv * pairs > INT32_MAX / 2) {
     return false;
   }
   const int64_t ints = (plan_ints(pairs, wgs) + 63) / 64 * 64;  // 256-byte aligned floats after
-  const int64_t rows = int64_t(wgs) * 2 * prefill_rows(head_dim);
+  const int64_t rows = int64_t(wgs) * 2 * prefill_rows(head_dim, true);
   *max_pairs = pairs;
   *bytes = ints * 4 + rows * (head_dim + 2) * 4;
   return true;
@@ -936,8 +998,9 @@ extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q
   a.page_shift = (page_size & (page_size - 1)) == 0 ? __builtin_ctz(unsigned(page_size)) : -1;
   a.max_blocks = max_blocks_per_seq;
   a.causal = causal ? 1 : 0;
-  a.tq = prefill_rows(head_dim) / a.group;
-  a.key_tile = 16 * kPrefillSubTiles;
+  const bool balanced = workspace != nullptr && workspace_bytes > 0;
+  a.tq = prefill_rows(head_dim, balanced) / a.group;
+  a.key_tile = prefill_key_tile(head_dim, balanced);
   a.scale_log2 = float(1.4426950408889634 / sqrt(double(head_dim)));
   a.balanced_wgs = 0;
   a.max_pairs = 0;
@@ -945,7 +1008,7 @@ extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q
   a.plan = nullptr;
   a.part_o = nullptr;
   a.part_ml = nullptr;
-  if (workspace != nullptr && workspace_bytes > 0) {
+  if (balanced) {
     const int wgs = head_dim == 256 ? (bf16 ? balanced_wgs<256, Bf16>() : balanced_wgs<256, F16>())
                                     : (bf16 ? balanced_wgs<128, Bf16>() : balanced_wgs<128, F16>());
     int64_t pairs = 0, need = 0;
@@ -963,13 +1026,21 @@ extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q
     a.plan = static_cast<int32_t*>(workspace);
     const int64_t ints = (plan_ints(pairs, wgs) + 63) / 64 * 64;
     a.part_o = reinterpret_cast<float*>(a.plan + ints);
-    a.part_ml = a.part_o + int64_t(wgs) * 2 * prefill_rows(head_dim) * head_dim;
+    a.part_ml = a.part_o + int64_t(wgs) * 2 * prefill_rows(head_dim, true) * head_dim;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (head_dim == 256) {
-    return bf16 ? launch_prefill<256, Bf16>(a, batch, max_seqlen_q, s)
-                : launch_prefill<256, F16>(a, batch, max_seqlen_q, s);
+    if (balanced) {
+      return bf16 ? launch_prefill<256, true, Bf16>(a, batch, max_seqlen_q, s)
+                  : launch_prefill<256, true, F16>(a, batch, max_seqlen_q, s);
+    }
+    return bf16 ? launch_prefill<256, false, Bf16>(a, batch, max_seqlen_q, s)
+                : launch_prefill<256, false, F16>(a, batch, max_seqlen_q, s);
   }
-  return bf16 ? launch_prefill<128, Bf16>(a, batch, max_seqlen_q, s)
-              : launch_prefill<128, F16>(a, batch, max_seqlen_q, s);
+  if (balanced) {
+    return bf16 ? launch_prefill<128, true, Bf16>(a, batch, max_seqlen_q, s)
+                : launch_prefill<128, true, F16>(a, batch, max_seqlen_q, s);
+  }
+  return bf16 ? launch_prefill<128, false, Bf16>(a, batch, max_seqlen_q, s)
+              : launch_prefill<128, false, F16>(a, batch, max_seqlen_q, s);
 }
