@@ -61,6 +61,27 @@ constexpr int kUnitCost = 2;          // a unit's start-up and epilogue, priced 
 static_assert(kMinChunkTiles > kUnitCost, "every balanced run must reach a key tile");
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// One 1 KiB load into LDS: lane i's 16 bytes at rsrc + voff land at LDS byte lds + 16 i. Issued
+// as assembly, which the compiler's wait insertion does not see: its own waits for the loads it
+// knows stay at least as strict (vector memory operations complete in issue order, so hidden
+// loads only add to what a count waits for), and the kernel waits for these loads explicitly
+// before each stage barrier. The builtin form instead makes the compiler wait for every load
+// into a stage array before reading that array, all loads issued since included, which defeats
+// a pipeline that keeps two tiles in flight.
+__device__ __forceinline__ void load_lds16(u32x4 rsrc, uint32_t voff, const uint16_t* lds) {
+  const uint32_t m0 = uint32_t(reinterpret_cast<uintptr_t>((lds_ptr_t)(lds)));
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(m0)
+               : "memory");
+}
+
+// Buffer descriptor words of [base, base + bytes) (raw, no stride), uniform.
+__device__ __forceinline__ u32x4 rsrc_words(const uint16_t* base, uint32_t bytes) {
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  return u32x4{uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(addr)))),
+               uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(addr >> 32) & 0xffffu))),
+               uint32_t(__builtin_amdgcn_readfirstlane(int(bytes))), uint32_t(kBufferRsrcWord3)};
+}
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -282,6 +303,9 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   // computed per read, K operands read through a ring, load offsets recomputed per tile. Each
   // costs the 8-wave shape 1-3 % (same-process A/B), which therefore keeps the plain forms.
   constexpr bool kLean = W > 8;
+  // K/V loads into LDS as assembly (load_lds16) or through the compiler's builtin: the 8-wave
+  // shape gains 3-6 % from the former, the 12-wave one loses ~3 % (same-process A/Bs).
+  constexpr bool kAsmLoads = !kLean;
   static_assert(LPW * RPB * LW == kKT && 16 % (kKT / LW) == 0,
                 "each wave's loads must lie inside one sub-tile");
 
@@ -384,25 +408,42 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
                          int64_t(key0 - page_of(key0) * a.page_size) * a.row_stride +
                          int64_t(kvh) * D;
     const uint32_t nbytes = rows > 0 ? uint32_t(rows - 1) * row_bytes + D * 2 : 0u;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k_cache + base, nbytes);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v_cache + base, nbytes);
     if (wave >= LW) return;  // uniform
     // Lean form: the per-lane offsets are recomputed at every fetch (an opaque copy of the lane
     // index keeps the compiler from hoisting 2 * LPW of them out of the loop, where they would
     // be spilled).
     int ln = lane;
     if constexpr (kLean) asm volatile("" : "+v"(ln));
-#pragma unroll
-    for (int i = 0; i < LPW; ++i) {
-      const int blk = wave * LPW + i;                  // 1 KiB block of the tile (uniform)
+    // Byte offsets of this lane's chunk of 1 KiB block blk of the tile in K and V.
+    auto chunk_offsets = [&](int blk, uint32_t& off_k, uint32_t& off_v)
+        __attribute__((always_inline)) {
       const int row = blk * RPB + ln / CPR;            // tile row of this lane's chunk
       const int slot = ln % CPR;
-      const int chunk_k = slot ^ lds_swizzle(row);
-      const int chunk_v = slot ^ lds_swizzle_v(row);
-      const uint32_t off_k = uint32_t(row & 15) * row_bytes + uint32_t(chunk_k) * 16u;
-      const uint32_t off_v = uint32_t(row & 15) * row_bytes + uint32_t(chunk_v) * 16u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(sk + blk * 512), 16, off_k, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(sv + blk * 512), 16, off_v, 0, 0, 0);
+      off_k = uint32_t(row & 15) * row_bytes + uint32_t(slot ^ lds_swizzle(row)) * 16u;
+      off_v = uint32_t(row & 15) * row_bytes + uint32_t(slot ^ lds_swizzle_v(row)) * 16u;
+    };
+    if constexpr (kAsmLoads) {
+      const u32x4 rk = rsrc_words(a.k_cache + base, nbytes);
+      const u32x4 rv = rsrc_words(a.v_cache + base, nbytes);
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) {
+        const int blk = wave * LPW + i;                  // 1 KiB block of the tile (uniform)
+        uint32_t off_k, off_v;
+        chunk_offsets(blk, off_k, off_v);
+        load_lds16(rk, off_k, sk + blk * 512);
+        load_lds16(rv, off_v, sv + blk * 512);
+      }
+    } else {
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k_cache + base, nbytes);
+      const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v_cache + base, nbytes);
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) {
+        const int blk = wave * LPW + i;
+        uint32_t off_k, off_v;
+        chunk_offsets(blk, off_k, off_v);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(sk + blk * 512), 16, off_k, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(sv + blk * 512), 16, off_v, 0, 0, 0);
+      }
     }
   };
 
@@ -584,14 +625,24 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     // Every wave is done reading both stages (previous unit). LDS only: the previous unit's
     // output stores may still be in flight; they drain under this unit's first loads.
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // Q lands here, before the tile loads are issued: the compiler does not see loads issued as
+    // assembly, and its wait for Q at the first use, inside the tile loop, would also wait for
+    // them.
+    if constexpr (kAsmLoads) {
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) asm volatile("" : "+v"(qop[c][kk]));
+      }
+    }
     if (cnt > 0) {
       fetch(sk0, sv0, empty_st[0], t0 * kKT);
       if (cnt > 1) load_ids((t0 + 1) * kKT);
     }
-    // Two tiles per trip so that each stage is a compile-time array. Each wave loads only part of
-    // a stage, so before the barrier every wave must wait for its own K/V loads into LDS to land
-    // (vmcnt): the compiler's __syncthreads does not count those loads as writes to order, and
-    // its per-wave waits before the LDS reads cover only the reading wave's own part.
+    // Two tiles per trip so that each stage is a compile-time array. Each wave loads only part
+    // of a stage, so before the barrier every wave must wait for its own K/V loads into LDS to
+    // land (vmcnt): the compiler's __syncthreads does not count those loads as writes to order,
+    // and its per-wave waits before the LDS reads cover only the reading wave's own part.
     for (int it = 0; it < cnt; it += 2) {
       const int k0 = (t0 + it) * kKT;
       // Stage 0 holds tile it; every wave is done with stage 1.
