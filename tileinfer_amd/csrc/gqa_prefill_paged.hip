@@ -296,7 +296,12 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int NT = D / 16;
   constexpr int CPR = D / 8;              // 16-byte chunks per row
   constexpr int RPB = 1024 / (2 * D);     // rows per 1 KiB load (64 lanes x 16 bytes)
-  constexpr int LW = W < 8 ? W : 8;       // waves that load the tiles (the others only compute)
+  // Waves 0-3 load the tiles; the others only compute. A wave issuing its loads stalls until the
+  // texture path takes them (~500-1000 cycles per tile when 8 waves issue together), and the
+  // SIMDs favour older waves, so the youngest waves set the pace of the stage barriers: loads go
+  // to the oldest waves, which wait at the barriers longest (per-wave s_memtime stamps; 4 waves
+  // loading: -6 % for 8-wave units, -3 % for 12-wave ones, against 8 waves loading).
+  constexpr int LW = 4;
   constexpr int LPW = kKT / RPB / LW;     // 1 KiB loads per loading wave per tile, each of K and V
   constexpr int ROWS = 16 * C * W;        // rows of the workgroup
   // Register-lean forms for shapes above 8 waves (3 waves per SIMD leave 168 VGPRs): V offsets
@@ -306,7 +311,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   // K/V loads into LDS as assembly (load_lds16) or through the compiler's builtin: the 8-wave
   // shape gains 3-6 % from the former, the 12-wave one loses ~3 % (same-process A/Bs).
   constexpr bool kAsmLoads = !kLean;
-  static_assert(LPW * RPB * LW == kKT && 16 % (kKT / LW) == 0,
+  static_assert(W >= LW && LPW * RPB * LW == kKT && 16 % (kKT / LW) == 0,
                 "each wave's loads must lie inside one sub-tile");
 
   __shared__ __align__(1024) uint16_t sk0[kKT * D];
