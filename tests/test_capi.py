@@ -127,8 +127,9 @@ def test_prefill_argument_errors_without_device():
 
 
 def test_prefill_workspace_sizes():
-    """The balanced schedule's workspace: plan tables plus two partial slots of 128 rows (head_dim
-    256; 256 rows at 128) per resident workgroup; none past the schedule's sequence limit."""
+    """The balanced schedule's workspace: plan tables plus two partial slots of 192 rows (head_dim
+    256, 12-wave workgroups; 256 rows at 128) per resident workgroup; none past the schedule's
+    sequence limit."""
     lib = _lib.load()
     out = ctypes.c_int64(-1)
 
@@ -137,7 +138,7 @@ def test_prefill_workspace_sizes():
                                                   ctypes.byref(out)) == _lib.TI_OK
         return out.value
     one = ws(1, 2048)
-    assert one > 256 * 2 * 128 * 256 * 4            # at least one round of partial slots
+    assert one > 256 * 2 * 192 * 256 * 4            # at least one round of partial slots
     assert ws(2, 2048) >= one                       # more pairs, more table rows
     assert ws(8193, 9000) == 0                      # beyond the schedule: run without one
     assert ws(1, 0) == 0
