@@ -178,6 +178,26 @@ int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                          int32_t causal, int32_t dtype, void* stream);
 
 /*
+ * ti_gqa_prefill_paged with the sigmoid gate in its output epilogue:
+ *   out[t, h, :] = prefill(t, h) * sigmoid(gate[t * gate_stride_t + h * gate_stride_h + :])
+ * bitwise what ti_gqa_prefill_paged followed by ti_sigmoid_mul gives (attention output rounded to
+ * the storage type first, as the unfused pair does), without the extra pass over the output. The
+ * gate of model/qwen_36.py:1083 on the prefill path is q_gate [1, q_len, H_q * D]
+ * (gate_stride_t = H_q * D, gate_stride_h = D); gate rows 16-byte aligned. Both schedules.
+ */
+int ti_gqa_prefill_paged_gated(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                               const void* k_cache, const void* v_cache,
+                               const int32_t* block_table, int64_t block_table_stride,
+                               const int32_t* cu_seqlens_q, const int32_t* seqlen_k, void* out,
+                               int64_t out_stride_t, int64_t out_stride_h, void* workspace,
+                               int64_t workspace_bytes, int32_t batch, int32_t total_q,
+                               int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
+                               int32_t head_dim, int32_t page_size, int64_t num_blocks,
+                               int32_t max_blocks_per_seq, int32_t causal, int32_t dtype,
+                               const void* gate, int64_t gate_stride_t, int64_t gate_stride_h,
+                               void* stream);
+
+/*
  * Workspace of the balanced ti_gqa_prefill_paged schedule for these sizes (host-only, no device
  * work). *bytes_out = 0 when the call must run without one (more than 8192 sequences, or tile
  * counts past int32). No reference counterpart (the reference's varlen kernel takes no workspace).

@@ -1,6 +1,7 @@
 """The fusions on either side of the path, through the C ABI: QK-norm + RoPE (+ append) against
 the oracle, the fused append bitwise against the unfused kernels, the sigmoid gate, and decode
-with the gate in its epilogue bitwise against decode followed by the gate."""
+with the gate in its epilogue bitwise against decode followed by the gate, and the same for the
+paged prefill."""
 import pytest
 import torch
 
@@ -8,7 +9,8 @@ from helpers import bits, say
 from oracle.ref_torch import ref_qknorm_rope, ref_qknorm_rope_fp32, ref_sigmoid_mul
 from tileinfer_amd.kernels import (fused_qknorm_rope, fused_sigmoid_mul, gqa_decode_paged_fn,
                                    qknorm_rope, qknorm_rope_append, store_kvcache)
-from tileinfer_amd.workloads import make_step
+from tileinfer_amd.kernels.gqa_prefill_paged import gqa_prefill_paged_fn
+from tileinfer_amd.workloads import make_step, prefill_step
 
 pytestmark = pytest.mark.gpu
 
@@ -116,4 +118,27 @@ def test_gated_decode_equals_decode_then_gate(ctx, split, dev):
     plain = gqa_decode_paged_fn(*args, split_tokens=split)
     gated = gqa_decode_paged_fn(*args, split_tokens=split, gate=gate)
     ref = fused_sigmoid_mul(plain, gate.view(len(ctx), 24, 256))
+    assert torch.equal(bits(gated), bits(ref))
+
+
+@pytest.mark.parametrize("schedule", ["balanced", "per_unit"])
+@pytest.mark.parametrize("q_lens,kv_lens,d,hq,hkv", [
+    ([300, 7, 0, 129], [900, 7, 5, 2000], 256, 24, 4),   # cut units, a whole one, an empty chunk
+    ([2048], [8192], 256, 24, 4),                        # config 4's continuation chunk
+    ([100, 33], [600, 33], 128, 16, 2),
+])
+def test_gated_prefill_equals_prefill_then_gate(q_lens, kv_lens, d, hq, hkv, schedule, dev):
+    """Prefill with the gate in its epilogue = prefill, then fused_sigmoid_mul: bitwise, for rows
+    the attention kernel stores and rows the merge kernel stores (balanced schedule), with the
+    gate as the model holds it (q_gate [1, total_q, H_q * D])."""
+    say(f"gated prefill q_lens={q_lens} kv_lens={kv_lens} d={d} schedule={schedule}")
+    step = prefill_step(q_lens, kv_lens, seed=32, hq=hq, hkv=hkv, d=d)
+    total_q = step.q.shape[0]
+    g = torch.Generator().manual_seed(6)
+    gate = (3 * torch.randn(1, total_q, hq * d, generator=g)).to(torch.bfloat16).to(dev)
+    args = (step.q.to(dev), step.k_cache.to(dev), step.v_cache.to(dev), step.block_table.to(dev),
+            step.cu_seqlens_q.to(dev), step.seqlen_k.to(dev), step.max_seqlen_q, step.page_size)
+    plain = gqa_prefill_paged_fn(*args, schedule=schedule)
+    gated = gqa_prefill_paged_fn(*args, schedule=schedule, gate=gate)
+    ref = fused_sigmoid_mul(plain, gate.view(total_q, hq, d))
     assert torch.equal(bits(gated), bits(ref))

@@ -52,6 +52,10 @@ struct PrefillArgs {
   int32_t* plan;   // schedule tables
   float* part_o;   // [balanced_wgs][2][rows][D] unnormalised partial rows
   float* part_ml;  // [balanced_wgs][2][rows][2] their (m, l), m in exp2 units
+  // Optional sigmoid gate of the output (out = attention * sigmoid(gate)), [total_q, hq, D] at
+  // these strides; nullptr for the plain output.
+  const uint16_t* gate;
+  int64_t gate_st, gate_sh;
 };
 
 constexpr float kRescaleSlack = 8.f;  // exp2 units a row maximum may rise before O is rescaled
@@ -681,11 +685,19 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
           a.out + int64_t(sx.q_start + qb0 + tok) * a.o_st + int64_t(kvh * G + hh) * a.o_sh;
       const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
       // Lane (n, g) holds d = 16 dt + 4g .. +3 of its row in o[c][dt].
+      const uint16_t* grow = a.gate ? a.gate + int64_t(sx.q_start + qb0 + tok) * a.gate_st +
+                                          int64_t(kvh * G + hh) * a.gate_sh
+                                    : nullptr;
 #pragma unroll
       for (int dt = 0; dt < NT; ++dt) {
         u32x2 w;
         w[0] = pack2(o[c][dt][0] * inv, o[c][dt][1] * inv, Tag{});
         w[1] = pack2(o[c][dt][2] * inv, o[c][dt][3] * inv, Tag{});
+        if (grow) {  // uniform
+          const u32x2 gv = *reinterpret_cast<const u32x2*>(grow + 16 * dt + 4 * g);
+          w[0] = gate_mul2(w[0], gv[0], Tag{});
+          w[1] = gate_mul2(w[1], gv[1], Tag{});
+        }
         *reinterpret_cast<u32x2*>(orow + 16 * dt + 4 * g) = w;
       }
     }
@@ -860,6 +872,13 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
     w[1] = pack2(acc[j][0][2] * inv, acc[j][0][3] * inv, Tag{});
     w[2] = pack2(acc[j][1][0] * inv, acc[j][1][1] * inv, Tag{});
     w[3] = pack2(acc[j][1][2] * inv, acc[j][1][3] * inv, Tag{});
+    if (a.gate) {
+      const u32x4 gv = *reinterpret_cast<const u32x4*>(
+          a.gate + int64_t(sx.q_start + qb0 + tok) * a.gate_st +
+          int64_t(kvh * a.group + hh) * a.gate_sh + d0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = gate_mul2(w[e], gv[e], Tag{});
+    }
     *reinterpret_cast<u32x4*>(orow) = w;
   }
 }
@@ -987,17 +1006,18 @@ extern "C" int ti_gqa_prefill_workspace_bytes(int32_t batch, int32_t total_q, in
   return TI_OK;
 }
 
-extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h,
-                                    const void* k_cache, const void* v_cache,
-                                    const int32_t* block_table, int64_t block_table_stride,
-                                    const int32_t* cu_seqlens_q, const int32_t* seqlen_k,
-                                    void* out, int64_t out_stride_t, int64_t out_stride_h,
-                                    void* workspace, int64_t workspace_bytes, int32_t batch,
-                                    int32_t total_q, int32_t max_seqlen_q, int32_t num_q_heads,
-                                    int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
-                                    int64_t num_blocks, int32_t max_blocks_per_seq, int32_t causal,
-                                    int32_t dtype, void* stream) {
-  using namespace ti;
+namespace ti {
+namespace {
+
+// Both entry points: gate == nullptr for the plain output.
+int prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                  const void* v_cache, const int32_t* block_table, int64_t block_table_stride,
+                  const int32_t* cu_seqlens_q, const int32_t* seqlen_k, void* out,
+                  int64_t out_stride_t, int64_t out_stride_h, void* workspace,
+                  int64_t workspace_bytes, int32_t batch, int32_t total_q, int32_t max_seqlen_q,
+                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                  int64_t num_blocks, int32_t max_blocks_per_seq, int32_t causal, int32_t dtype,
+                  void* stream, const void* gate, int64_t gate_stride_t, int64_t gate_stride_h) {
   if (dtype != TI_DTYPE_BF16 && dtype != TI_DTYPE_F16) {
     return fail(TI_EUNSUPPORTED, "ti_gqa_prefill_paged: dtype code %d is not bf16/fp16", dtype);
   }
@@ -1028,6 +1048,9 @@ extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q
       (reinterpret_cast<uintptr_t>(v_cache) & 15) ||
       (reinterpret_cast<uintptr_t>(workspace) & 255)) {
     return fail(TI_EINVAL, "ti_gqa_prefill_paged: rows must be 16-byte aligned (workspace 256)");
+  }
+  if (gate && ((reinterpret_cast<uintptr_t>(gate) & 15) || gate_stride_t % 8 || gate_stride_h % 8)) {
+    return fail(TI_EINVAL, "ti_gqa_prefill_paged_gated: gate rows must be 16-byte aligned");
   }
   const bool bf16 = dtype == TI_DTYPE_BF16;
   PrefillArgs a;
@@ -1064,6 +1087,9 @@ extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q
   a.plan = nullptr;
   a.part_o = nullptr;
   a.part_ml = nullptr;
+  a.gate = static_cast<const uint16_t*>(gate);
+  a.gate_st = gate_stride_t;
+  a.gate_sh = gate_stride_h;
   if (balanced) {
     const int wgs = head_dim == 256 ? (bf16 ? balanced_wgs<256, Bf16>() : balanced_wgs<256, F16>())
                                     : (bf16 ? balanced_wgs<128, Bf16>() : balanced_wgs<128, F16>());
@@ -1099,4 +1125,41 @@ extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q
   }
   return bf16 ? launch_prefill<128, false, Bf16>(a, batch, max_seqlen_q, s)
               : launch_prefill<128, false, F16>(a, batch, max_seqlen_q, s);
+}
+
+}  // namespace
+}  // namespace ti
+
+extern "C" int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                    const void* k_cache, const void* v_cache,
+                                    const int32_t* block_table, int64_t block_table_stride,
+                                    const int32_t* cu_seqlens_q, const int32_t* seqlen_k,
+                                    void* out, int64_t out_stride_t, int64_t out_stride_h,
+                                    void* workspace, int64_t workspace_bytes, int32_t batch,
+                                    int32_t total_q, int32_t max_seqlen_q, int32_t num_q_heads,
+                                    int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                    int64_t num_blocks, int32_t max_blocks_per_seq, int32_t causal,
+                                    int32_t dtype, void* stream) {
+  return ti::prefill_paged(q, q_stride_t, q_stride_h, k_cache, v_cache, block_table,
+                           block_table_stride, cu_seqlens_q, seqlen_k, out, out_stride_t,
+                           out_stride_h, workspace, workspace_bytes, batch, total_q, max_seqlen_q,
+                           num_q_heads, num_kv_heads, head_dim, page_size, num_blocks,
+                           max_blocks_per_seq, causal, dtype, stream, nullptr, 0, 0);
+}
+
+extern "C" int ti_gqa_prefill_paged_gated(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+    const void* v_cache, const int32_t* block_table, int64_t block_table_stride,
+    const int32_t* cu_seqlens_q, const int32_t* seqlen_k, void* out, int64_t out_stride_t,
+    int64_t out_stride_h, void* workspace, int64_t workspace_bytes, int32_t batch, int32_t total_q,
+    int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t page_size, int64_t num_blocks, int32_t max_blocks_per_seq, int32_t causal,
+    int32_t dtype, const void* gate, int64_t gate_stride_t, int64_t gate_stride_h, void* stream) {
+  if (!gate) return ti::fail(TI_EINVAL, "ti_gqa_prefill_paged_gated: null gate");
+  return ti::prefill_paged(q, q_stride_t, q_stride_h, k_cache, v_cache, block_table,
+                           block_table_stride, cu_seqlens_q, seqlen_k, out, out_stride_t,
+                           out_stride_h, workspace, workspace_bytes, batch, total_q, max_seqlen_q,
+                           num_q_heads, num_kv_heads, head_dim, page_size, num_blocks,
+                           max_blocks_per_seq, causal, dtype, stream, gate, gate_stride_t,
+                           gate_stride_h);
 }

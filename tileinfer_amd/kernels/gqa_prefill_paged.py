@@ -111,6 +111,7 @@ def gqa_prefill_paged_fn(
     batch_invariant: bool = False,
     max_seqlen_k: int | None = None,
     schedule: str = "auto",
+    gate: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Varlen (causal) GQA attention of packed queries over paged K/V.
 
@@ -131,6 +132,10 @@ def gqa_prefill_paged_fn(
         max_seqlen_k: keyword-only host bound on every ``seqlen_k`` (the reference's
             ``ctx.max_seqlen_k``); only used to choose the schedule
         schedule: keyword-only, "auto", "balanced" or "per_unit" (see the module docstring)
+        gate: keyword-only; the attention output gate (model/qwen_36.py:1083), total_q * H_q * D
+            values laid out [total_q, H_q, D] (``q_gate`` [1, q_len, H_q * D] as the model has it):
+            the output is ``prefill * sigmoid(gate)``, applied in the kernels' epilogue — bitwise
+            ``fused_sigmoid_mul(gqa_prefill_paged_fn(...), gate)``.
     Returns:
         [total_q, H_q, D] tensor in q's dtype.
     """
@@ -191,6 +196,13 @@ def gqa_prefill_paged_fn(
           or not _aligned_rows(out)):
         raise ValueError("out must be a [total_q, H_q, D] tensor of q's dtype and device with "
                          "16-byte aligned rows")
+    g3 = None
+    if gate is not None:
+        if gate.numel() != total_q * h_q * d or gate.dtype != dt or gate.device != dev:
+            raise ValueError(f"gate must hold {total_q}x{h_q}x{d} values of q's dtype on q's device")
+        g3 = gate.reshape(total_q, h_q, d)
+        if not _aligned_rows(g3):
+            g3 = g3.contiguous()
     if batch == 0 or total_q == 0:
         return out
     width = block_table.shape[1]
@@ -205,11 +217,15 @@ def gqa_prefill_paged_fn(
         ws_bytes = _workspace_bytes(batch, total_q, h_q, h_kv, d, page_size, width)
         if ws_bytes > 0:
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    _lib.check(lib.ti_gqa_prefill_paged(
-        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
-        block_table.data_ptr(), block_table.stride(0) if width > 0 else 0,
-        cu_seqlens_q.data_ptr(), seqlen_k.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
-        ws.data_ptr() if ws is not None else None, ws_bytes,
-        batch, total_q, max_seqlen_q, h_q, h_kv, d, page_size, rows // page_size, width,
-        1 if causal else 0, code, _lib.stream_handle(dev)))
+    args = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+            block_table.data_ptr(), block_table.stride(0) if width > 0 else 0,
+            cu_seqlens_q.data_ptr(), seqlen_k.data_ptr(), out.data_ptr(), out.stride(0),
+            out.stride(1), ws.data_ptr() if ws is not None else None, ws_bytes,
+            batch, total_q, max_seqlen_q, h_q, h_kv, d, page_size, rows // page_size, width,
+            1 if causal else 0, code)
+    if g3 is None:
+        _lib.check(lib.ti_gqa_prefill_paged(*args, _lib.stream_handle(dev)))
+    else:
+        _lib.check(lib.ti_gqa_prefill_paged_gated(*args, g3.data_ptr(), g3.stride(0), g3.stride(1),
+                                                  _lib.stream_handle(dev)))
     return out
