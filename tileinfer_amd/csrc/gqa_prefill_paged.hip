@@ -752,7 +752,12 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     pos = int64_t(i) * chunk;
     end = min(pos + chunk, total);
   }
-  bool first = true;
+  // A run that starts inside a unit defers that first piece (the unit's tail) to its end: every
+  // run then starts at key 0 of a unit, and the deferred tail begins about where the run's last
+  // piece (the next unit's head, same cut) ended, so an XCD's workgroups sweep the keys together
+  // and share pages in L2. Partial slot 0 stays the run's first piece, slot 1 its last.
+  bool first = true, deferred = false, replay = false;
+  int d_p = 0, d_kvh = 0;
   for (;;) {
     int nt = grid_nt, t0 = 0, t1 = grid_nt;
     bool last = true;
@@ -767,17 +772,32 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       t1 = int(min(end - k_pos, int64_t(nt)));
       last = k_pos + nt >= end;
     }
+    const bool slot0 = first || replay;
     // Units without keys get their zero rows from the merge (balanced) or here (grid: nt = 0).
-    if (t0 < t1 || !balanced) {
+    bool go = t0 < t1 || !balanced;
+    if (go && first && t0 > 0 && !last) {  // balanced only (grid units start at 0)
+      d_p = p;
+      d_kvh = kvh;
+      deferred = true;
+      first = false;
+      go = false;
+    }
+    if (go) {
       run_unit(t0, t1);
       if (t0 == 0 && t1 == nt) store_final();
-      else store_partial((int64_t(i) * 2 + (first ? 0 : 1)) * ROWS);
+      else store_partial((int64_t(i) * 2 + (slot0 ? 0 : 1)) * ROWS);
       first = false;
     }
-    if (last) break;
-    if (++p == n_pairs) {
+    bool done = last || replay;
+    if (!done && ++p == n_pairs) {
       p = 0;
-      if (++kvh == a.hkv) break;
+      done = ++kvh == a.hkv;
+    }
+    if (done) {
+      if (!deferred || replay) break;
+      p = d_p;
+      kvh = d_kvh;
+      replay = true;
     }
   }
 }
