@@ -255,23 +255,23 @@ def test_many_sequences_vs_oracle(invariant, dev):
     close(run_gpu(step, dev, schedule=SCHED[invariant]), run_ref(step))
 
 
-def paged_step(q_lens, kv_lens, page, seed):
+def paged_step(q_lens, kv_lens, page, seed, hq=24, hkv=4, d=256, dtype=torch.bfloat16):
     """A prefill step whose cache pages hold `page` rows (the flattened layout is the same)."""
     g = torch.Generator().manual_seed(seed)
     need = sum((n + page - 1) // page for n in kv_lens)
     pool = need + 5
     perm = torch.randperm(pool, generator=g).to(torch.int32)
-    width = max((n + page - 1) // page for n in kv_lens)
+    width = max(1, max((n + page - 1) // page for n in kv_lens))
     table = torch.full((len(kv_lens), width), -1, dtype=torch.int32)
     at = 0
     for b, n in enumerate(kv_lens):
         k = (n + page - 1) // page
         table[b, :k] = perm[at:at + k]
         at += k
-    kc = torch.randn(pool, page, 4, 256, generator=g).to(torch.bfloat16)
-    vc = torch.randn(pool, page, 4, 256, generator=g).to(torch.bfloat16)
+    kc = torch.randn(pool, page, hkv, d, generator=g).to(dtype)
+    vc = torch.randn(pool, page, hkv, d, generator=g).to(dtype)
     cu = torch.tensor([0] + list(torch.tensor(q_lens).cumsum(0)), dtype=torch.int32)
-    q = torch.randn(int(cu[-1]), 24, 256, generator=g).to(torch.bfloat16)
+    q = torch.randn(int(cu[-1]), hq, d, generator=g).to(dtype)
     return q, kc, vc, table, cu, torch.tensor(kv_lens, dtype=torch.int32)
 
 
@@ -303,3 +303,33 @@ def test_repeated_calls_bitwise_identical(invariant, dev):
     first = bits(gqa_prefill_paged_fn(*args, schedule=SCHED[invariant]))
     for _ in range(23):
         assert torch.equal(bits(gqa_prefill_paged_fn(*args, schedule=SCHED[invariant])), first)
+
+
+def _random_case(seed):
+    """A seeded random call: batch 1-4, chunk and context lengths, GQA group (including groups
+    that do not divide the workgroup's rows), head_dim, dtype, page size, causal or not."""
+    g = torch.Generator().manual_seed(seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=g))]  # noqa: E731
+    hkv = pick([1, 2, 4])
+    group = pick([1, 3, 5, 6, 7, 8, 12])
+    d = pick([128, 256])
+    batch = int(torch.randint(1, 5, (1,), generator=g))
+    q_lens = [int(torch.randint(0, 160, (1,), generator=g)) for _ in range(batch)]
+    kv_lens = [q + int(torch.randint(0, 900, (1,), generator=g)) for q in q_lens]
+    return dict(q_lens=q_lens, kv_lens=kv_lens, hq=hkv * group, hkv=hkv, d=d,
+                dtype=pick([torch.bfloat16, torch.float16]), page=pick([16, 32]),
+                causal=bool(torch.randint(2, (1,), generator=g)))
+
+
+@pytest.mark.parametrize("seed", range(100, 116))
+def test_random_calls_vs_oracle(seed, dev):
+    """Seeded random calls through both schedules against the oracle."""
+    c = _random_case(seed)
+    say(f"prefill random seed={seed} {c}")
+    q, kc, vc, table, cu, sk = paged_step(c["q_lens"], c["kv_lens"], c["page"], seed, hq=c["hq"],
+                                          hkv=c["hkv"], d=c["d"], dtype=c["dtype"])
+    ref = ref_gqa_prefill_paged(q, kc, vc, table, cu, sk, c["page"], c["causal"])
+    args = (q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), cu.to(dev), sk.to(dev),
+            max(c["q_lens"]), c["page"])
+    for schedule in ("balanced", "per_unit"):
+        close(gqa_prefill_paged_fn(*args, causal=c["causal"], schedule=schedule), ref)
