@@ -261,3 +261,38 @@ def test_larger_pages_vs_oracle(page, dev):
     seq = torch.tensor(ctx, dtype=torch.int32)
     out = gqa_decode_paged_fn(q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), seq.to(dev), page)
     assert_decode_close(out, ref_gqa_decode_paged(q, kc, vc, table, seq, page))
+
+
+@pytest.mark.parametrize("seed", range(200, 216))
+def test_random_calls_vs_oracle(seed, dev):
+    """Seeded random calls against the oracle: batch 1-6 with contexts 0-3,000, GQA groups 1-16,
+    1-8 KV heads, head_dim 128/256, bf16/fp16, pages of 16/32/48 rows, the balanced plan and fixed
+    splits, the MFMA and (groups 4, 6, 8) the scalar variants."""
+    g = torch.Generator().manual_seed(seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=g))]  # noqa: E731
+    hkv, group, d = pick([1, 2, 4, 8]), pick([1, 2, 3, 5, 6, 8, 11, 16]), pick([128, 256])
+    dtype, page = pick([torch.bfloat16, torch.float16]), pick([16, 32, 48])
+    unit = 32 * page // math.gcd(32, page)             # fixed splits are multiples of lcm(32, page)
+    split = pick([None, None, unit, 8 * unit])
+    batch = int(torch.randint(1, 7, (1,), generator=g))
+    ctx = [int(torch.randint(0, 3001, (1,), generator=g)) for _ in range(batch)]
+    say(f"decode random seed={seed} ctx={ctx} hkv={hkv} group={group} d={d} page={page} split={split}")
+    need = sum((n + page - 1) // page for n in ctx)
+    perm = torch.randperm(need + 3, generator=g).to(torch.int32)
+    width = max(1, max((n + page - 1) // page for n in ctx))
+    table = torch.full((len(ctx), width), -1, dtype=torch.int32)
+    at = 0
+    for b, n in enumerate(ctx):
+        k = (n + page - 1) // page
+        table[b, :k] = perm[at:at + k]
+        at += k
+    kc = torch.randn(need + 3, page, hkv, d, generator=g).to(dtype)
+    vc = torch.randn(need + 3, page, hkv, d, generator=g).to(dtype)
+    q = torch.randn(len(ctx), hkv * group, d, generator=g).to(dtype)
+    seqlen = torch.tensor(ctx, dtype=torch.int32)
+    ref = ref_gqa_decode_paged(q, kc, vc, table, seqlen, page)
+    # The scalar variant is built for groups of 4, 6 and 8 only.
+    for variant in VARIANTS if group in (4, 6, 8) else ["mfma"]:
+        out = gqa_decode_paged_fn(q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), seqlen.to(dev),
+                                  page, split_tokens=split, variant=variant)
+        assert_decode_close(out, ref)
