@@ -409,6 +409,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       empty |= (nbid[j] < 0 ? 1u : 0u) << j;
     }
     empty_out = empty;
+    if (wave >= LW) return;  // uniform: the other waves only need the mask
     bid = __builtin_amdgcn_readfirstlane(bid);
     const int key0 = k0 + 16 * my_sub;
     const int rows = __builtin_amdgcn_readfirstlane(bid < 0 ? 0 : sub_rows(key0));
@@ -417,7 +418,6 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
                          int64_t(key0 - page_of(key0) * a.page_size) * a.row_stride +
                          int64_t(kvh) * D;
     const uint32_t nbytes = rows > 0 ? uint32_t(rows - 1) * row_bytes + D * 2 : 0u;
-    if (wave >= LW) return;  // uniform
     // Lean form: the per-lane offsets are recomputed at every fetch (an opaque copy of the lane
     // index keeps the compiler from hoisting 2 * LPW of them out of the loop, where they would
     // be spilled).
