@@ -423,6 +423,11 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     // be spilled).
     int ln = lane;
     if constexpr (kLean) asm volatile("" : "+v"(ln));
+    // The wave's first 1 KiB block of the tile, recomputed at every fetch (an opaque copy of the
+    // wave index): hoisted out of the loop, the 2 * LPW LDS addresses would occupy scalar
+    // registers for the whole loop and be spilled.
+    int wblk = wave * LPW;
+    asm volatile("" : "+s"(wblk));
     // Byte offsets of this lane's chunk of 1 KiB block blk of the tile in K and V.
     auto chunk_offsets = [&](int blk, uint32_t& off_k, uint32_t& off_v)
         __attribute__((always_inline)) {
@@ -436,7 +441,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       const u32x4 rv = rsrc_words(a.v_cache + base, nbytes);
 #pragma unroll
       for (int i = 0; i < LPW; ++i) {
-        const int blk = wave * LPW + i;                  // 1 KiB block of the tile (uniform)
+        const int blk = wblk + i;                  // 1 KiB block of the tile (uniform)
         uint32_t off_k, off_v;
         chunk_offsets(blk, off_k, off_v);
         load_lds16(rk, off_k, sk + blk * 512);
@@ -447,7 +452,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v_cache + base, nbytes);
 #pragma unroll
       for (int i = 0; i < LPW; ++i) {
-        const int blk = wave * LPW + i;
+        const int blk = wblk + i;
         uint32_t off_k, off_v;
         chunk_offsets(blk, off_k, off_v);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(sk + blk * 512), 16, off_k, 0, 0, 0);
