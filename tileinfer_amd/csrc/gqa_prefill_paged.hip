@@ -157,9 +157,9 @@ __device__ __forceinline__ int block_key_end(const PrefillArgs& a, const SeqExte
 // workspace (int32):
 //   header   {pairs, work per KV head, chunk, total work}
 //   per pair {sequence, query block, key tiles, exclusive prefix of work}   (max_pairs each)
-//   per workgroup {KV head, pair, first key tile}                          (balanced_wgs each)
+//   per workgroup {KV head, pair} of its first unit                        (balanced_wgs each)
 struct PlanView {
-  int32_t *hdr, *pair_b, *pair_qb, *pair_nt, *pair_pre, *wg_kvh, *wg_p, *wg_t;
+  int32_t *hdr, *pair_b, *pair_qb, *pair_nt, *pair_pre, *wg_kvh, *wg_p;
 };
 
 __device__ __forceinline__ PlanView plan_view(const PrefillArgs& a) {
@@ -171,11 +171,10 @@ __device__ __forceinline__ PlanView plan_view(const PrefillArgs& a) {
   v.pair_pre = v.pair_nt + a.max_pairs;
   v.wg_kvh = v.pair_pre + a.max_pairs;
   v.wg_p = v.wg_kvh + a.balanced_wgs;
-  v.wg_t = v.wg_p + a.balanced_wgs;
   return v;
 }
 
-int64_t plan_ints(int64_t max_pairs, int64_t wgs) { return 4 + 4 * max_pairs + 3 * wgs; }
+int64_t plan_ints(int64_t max_pairs, int64_t wgs) { return 4 + 4 * max_pairs + 2 * wgs; }
 
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxPlanSeqs = 8192;  // sequences of one balanced launch (first pairs kept in LDS)
@@ -264,7 +263,7 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs 
   for (int i = t; i < wgs; i += kPlanThreads) v.wg_p[i] = -1;
   __syncthreads();  // the -1 defaults land before the starts below
   // Workgroup i starts in the unit holding work position i * chunk (units without key tiles
-  // hold none), at its first key tile when the position falls in the unit's fixed part.
+  // hold none; a position in a unit's fixed part starts that unit at its first key tile).
   const int units = a.hkv * n_pairs;
   for (int u = t; u < units; u += kPlanThreads) {
     const int kvh = u / n_pairs;
@@ -276,7 +275,6 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs 
          ++i) {
       v.wg_kvh[i] = kvh;
       v.wg_p[i] = p;
-      v.wg_t[i] = int32_t(max(i * chunk - pre - kUnitCost, int64_t(0)));
     }
   }
 }
