@@ -126,6 +126,21 @@ def test_prefill_argument_errors_without_device():
     assert rc == _lib.TI_EINVAL and b"null" in _lib.load().ti_last_error()
 
 
+def test_gated_prefill_argument_errors_without_device():
+    """The gated entry point: a null gate, or gate rows off 16-byte alignment, are rejected before
+    anything is launched (fake but aligned device addresses stand in for the tensors)."""
+    lib = _lib.load()
+    fake = 1 << 20
+
+    def call(gate, gate_st=24 * 256, gate_sh=256):
+        return lib.ti_gqa_prefill_paged_gated(fake, 24 * 256, 256, fake, fake, fake, 8, fake, fake,
+                                              fake, 24 * 256, 256, None, 0, 1, 4, 4, 24, 4, 256,
+                                              16, 64, 8, 1, 0, gate, gate_st, gate_sh, None)
+    assert call(None) == _lib.TI_EINVAL and b"null gate" in lib.ti_last_error()
+    assert call(fake + 8) == _lib.TI_EINVAL and b"gate" in lib.ti_last_error()
+    assert call(fake, gate_sh=4) == _lib.TI_EINVAL and b"gate" in lib.ti_last_error()
+
+
 def test_prefill_workspace_sizes():
     """The balanced schedule's workspace: plan tables plus two partial slots of 192 rows (head_dim
     256, 12-wave workgroups; 256 rows at 128) per resident workgroup; none past the schedule's
