@@ -333,3 +333,36 @@ def test_random_calls_vs_oracle(seed, dev):
             max(c["q_lens"]), c["page"])
     for schedule in ("balanced", "per_unit"):
         close(gqa_prefill_paged_fn(*args, causal=c["causal"], schedule=schedule), ref)
+
+
+@pytest.mark.parametrize("invariant", MODES)
+def test_graph_capture_replay(invariant, dev):
+    """The prefill (with its schedule and merge launches and the workspace from torch's graph
+    pool) captured in a HIP graph: every replay, with new queries and eager work between, matches
+    the eager result bitwise."""
+    say(f"prefill graph capture invariant={invariant}")
+    step = prefill_step([300, 77, 5], [1200, 77, 600], seed=33)
+    q = step.q.to(dev)
+    args = (step.k_cache.to(dev), step.v_cache.to(dev), step.block_table.to(dev),
+            step.cu_seqlens_q.to(dev), step.seqlen_k.to(dev), step.max_seqlen_q)
+
+    def fn():
+        return gqa_prefill_paged_fn(q, *args, schedule=SCHED[invariant])
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = fn()
+    gen = torch.Generator(device=dev).manual_seed(3)
+    for r in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen, device=dev).to(q.dtype))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = fn()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(static_out), bits(eager)), f"replay {r}"
