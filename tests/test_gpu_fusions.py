@@ -5,7 +5,7 @@ paged prefill."""
 import pytest
 import torch
 
-from helpers import bits, say
+from helpers import bits, flat, say
 from oracle.ref_torch import ref_qknorm_rope, ref_qknorm_rope_fp32, ref_sigmoid_mul
 from tileinfer_amd.kernels import (fused_qknorm_rope, fused_sigmoid_mul, gqa_decode_paged_fn,
                                    qknorm_rope, qknorm_rope_append, store_kvcache)
@@ -142,3 +142,45 @@ def test_gated_prefill_equals_prefill_then_gate(q_lens, kv_lens, d, hq, hkv, sch
     gated = gqa_prefill_paged_fn(*args, schedule=schedule, gate=gate)
     ref = fused_sigmoid_mul(plain, gate.view(total_q, hq, d))
     assert torch.equal(bits(gated), bits(ref))
+
+
+def test_fused_decode_step_graph_capture_replay(dev):
+    """A whole fused decode step — QK-norm + RoPE + append in one launch, then decode with the gate
+    in its epilogue — captured in a HIP graph: every replay, with new inputs and eager work
+    between, matches the eager step bitwise (outputs and cache)."""
+    say("fused decode step graph capture")
+    step = make_step([700, 33, 1500], pool=200, seed=34)
+    b = step.q.shape[0]
+    kc, vc = step.k_cache.to(dev), step.v_cache.to(dev)
+    q, k, v = step.q.to(dev), step.k_new.to(dev), step.v_new.to(dev)
+    _, qw = inputs(1, 1, 256, seed=5)
+    _, kw = inputs(1, 1, 256, seed=6)
+    qw, kw = qw.to(dev), kw.to(dev)
+    cos, sin = (x.to(dev) for x in angles(b, 64))
+    slots, tbl, seq = step.slot_mapping.to(dev), step.block_table.to(dev), step.seqlen.to(dev)
+    gate = torch.zeros(b, 1, 24 * 256, dtype=torch.bfloat16, device=dev)
+
+    def fn():
+        qo = qknorm_rope_append(q, k, v, qw, kw, cos, sin, flat(kc), flat(vc), slots)
+        return gqa_decode_paged_fn(qo, kc, vc, tbl, seq, gate=gate)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = fn()
+    gen = torch.Generator(device=dev).manual_seed(7)
+    for r in range(3):
+        for x in (q, k, v, gate):
+            x.copy_((2 * torch.randn(x.shape, generator=gen, device=dev)).to(x.dtype))
+        graph.replay()
+        torch.cuda.synchronize()
+        kc_g, vc_g, out_g = kc.clone(), vc.clone(), static_out.clone()
+        eager = fn()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(out_g), bits(eager)), f"replay {r}"
+        assert torch.equal(bits(kc_g), bits(kc)) and torch.equal(bits(vc_g), bits(vc)), f"cache {r}"
