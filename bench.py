@@ -457,7 +457,19 @@ def run_config(cfg: int, args, dev) -> dict:
         stream_us = _time(lambda: gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen,
                                                       split_tokens=args.split_tokens,
                                                       variant=args.variant), args.steps, args.warmup)
+        # The prefix attended once for the batch (the caller's statement that every sequence
+        # shares its first 8192 tokens), against the plain call's output.
+        prefix = st.meta["prefix_tokens"]
+        shared_fn = lambda: gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen,  # noqa: E731
+                                                 kv_reuse=True, shared_prefix_tokens=prefix)
+        shared_us = _time(shared_fn, args.steps, args.warmup)
+        plain = gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen, kv_reuse=True)
+        shared_err = float((shared_fn().float() - plain.float()).abs().max())
         extra = {"decode_us_streaming_policy": round(stream_us, 2),
+                 "decode_us_shared_prefix": round(shared_us, 2),
+                 "decode_GBps_logical_shared_prefix": round(d_bytes / (shared_us * 1e-6) / 1e9, 1),
+                 "shared_prefix_tokens": prefix,
+                 "shared_prefix_max_abs_diff_vs_plain": shared_err,
                  "swap": swap_config5(st, dev, args),
                  "decode_logical_bytes": d_bytes,
                  "decode_physical_unique_kv_bytes": unique * 2 * BLOCK * HKV * HEAD_DIM * 2,

@@ -198,6 +198,25 @@ int ti_gqa_prefill_paged_gated(const void* q, int64_t q_stride_t, int64_t q_stri
                                void* stream);
 
 /*
+ * ti_gqa_prefill_paged with unnormalised fp32 output, for merging with attention over other keys:
+ *   o_part  [total_q, num_q_heads, head_dim] fp32, o relative to 2^m (16-byte aligned)
+ *   ml_part [total_q, num_q_heads, 2] fp32 (m, l): m the running maximum of the scaled scores in
+ *           exp2 units (-inf: no visible key), l the sum of 2^(s - m)
+ * so that out = o_part / l. No reference counterpart: it is the prefix half of
+ * ti_gqa_decode_paged_prefixed (a shared prefix attended once for a whole decode batch).
+ */
+int ti_gqa_prefill_paged_partial(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                 const void* k_cache, const void* v_cache,
+                                 const int32_t* block_table, int64_t block_table_stride,
+                                 const int32_t* cu_seqlens_q, const int32_t* seqlen_k,
+                                 float* o_part, float* ml_part, void* workspace,
+                                 int64_t workspace_bytes, int32_t batch, int32_t total_q,
+                                 int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
+                                 int32_t head_dim, int32_t page_size, int64_t num_blocks,
+                                 int32_t max_blocks_per_seq, int32_t causal, int32_t dtype,
+                                 void* stream);
+
+/*
  * Workspace of the balanced ti_gqa_prefill_paged schedule for these sizes (host-only, no device
  * work). *bytes_out = 0 when the call must run without one (more than 8192 sequences, or tile
  * counts past int32). No reference counterpart (the reference's varlen kernel takes no workspace).
@@ -298,6 +317,30 @@ int ti_gqa_decode_paged_gated(const void* q, int64_t q_stride_b, int64_t q_strid
                               int32_t split_tokens, int32_t variant, int32_t dtype,
                               const void* gate, int64_t gate_stride_b, int64_t gate_stride_h,
                               void* stream);
+
+/*
+ * ti_gqa_decode_paged (optionally gated) for a batch whose sequences share their first
+ * prefix_tokens tokens (a multiple of page_size): the kernel attends to tokens
+ * [prefix_tokens, seqlen[b]) of each sequence, through block_table columns from
+ * prefix_tokens / page_size on, and merges into every row the precomputed prefix part
+ * (prefix_o [B, H_q, D], prefix_ml [B, H_q, 2], as ti_gqa_prefill_paged_partial writes them).
+ * Same arguments as ti_gqa_decode_paged_gated otherwise (gate may be NULL); the workspace is
+ * ti_gqa_decode_plan's for max_blocks_per_seq - prefix_tokens / page_size. MFMA variant only.
+ * Reference counterpart: gqa_decode_paged_fn (kernels/gqa_decode_paged.py:392-437) on a batch
+ * whose block tables share a prefix (engine/scheduler.py:161-189 share_blocks), which reads the
+ * shared pages once per sequence.
+ */
+int ti_gqa_decode_paged_prefixed(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                 const void* k_cache, const void* v_cache,
+                                 const int32_t* block_table, int64_t block_table_stride,
+                                 const int32_t* seqlen, void* out, void* workspace,
+                                 int64_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                 int64_t num_blocks, int32_t max_blocks_per_seq,
+                                 int32_t split_tokens, int32_t variant, int32_t dtype,
+                                 const void* gate, int64_t gate_stride_b, int64_t gate_stride_h,
+                                 const float* prefix_o, const float* prefix_ml,
+                                 int32_t prefix_tokens, void* stream);
 
 /* Text of the last error reported on the calling thread ("" when none). */
 const char* ti_last_error(void);

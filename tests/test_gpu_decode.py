@@ -296,3 +296,77 @@ def test_random_calls_vs_oracle(seed, dev):
         out = gqa_decode_paged_fn(q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), seqlen.to(dev),
                                   page, split_tokens=split, variant=variant)
         assert_decode_close(out, ref)
+
+
+def _shared_prefix_step(suffix, prefix, seed, hq=24, hkv=4, d=256, page=16):
+    """A batch whose sequences share their first `prefix` tokens: the shared layout (every table
+    aliases sequence 0's prefix pages) and a private one (each sequence has its own copy of the
+    same values)."""
+    g = torch.Generator().manual_seed(seed)
+    ctx = [prefix + s for s in suffix]
+    pp = prefix // page
+    own = [(c + page - 1) // page - pp for c in ctx]
+    pool = pp * (len(ctx) + 1) + sum(own) + 3
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    width = max(1, max((c + page - 1) // page for c in ctx))
+    shared = torch.full((len(ctx), width), -1, dtype=torch.int32)
+    private = shared.clone()
+    kc = torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16)
+    vc = torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16)
+    at = pp
+    prefix_ids = perm[:pp]
+    for b in range(len(ctx)):
+        shared[b, :pp] = prefix_ids
+        private[b, :pp] = perm[at:at + pp]
+        kc[perm[at:at + pp].long()] = kc[prefix_ids.long()]
+        vc[perm[at:at + pp].long()] = vc[prefix_ids.long()]
+        at += pp
+        shared[b, pp:pp + own[b]] = perm[at:at + own[b]]
+        private[b, pp:pp + own[b]] = perm[at:at + own[b]]
+        at += own[b]
+    q = torch.randn(len(ctx), hq, d, generator=g).to(torch.bfloat16)
+    return q, kc, vc, shared, private, torch.tensor(ctx, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("suffix,prefix,split", [
+    ([512] * 6, 2048, None),                     # config 5's shape, scaled down
+    ([0, 1, 700, 33, 4000, 16], 1024, None),     # empty and short suffixes, one cut over many runs
+    ([300, 300, 5], 512, 256),                   # a fixed split
+    ([90] * 40, 4096, None),                     # many sequences, long prefix
+])
+def test_shared_prefix_decode(suffix, prefix, split, dev):
+    """shared_prefix_tokens: the prefix attended once for the batch and merged into each row —
+    against the oracle and the plain call (tolerance), bitwise the same for the shared and the
+    private layout, and (gated) bitwise the unfused gate."""
+    say(f"decode shared prefix={prefix} suffix={suffix} split={split}")
+    q, kc, vc, shared, private, seq = _shared_prefix_step(suffix, prefix, seed=prefix + len(suffix))
+    ref = ref_gqa_decode_paged(q, kc, vc, shared, seq)
+    d_q, d_kc, d_vc, d_seq = q.to(dev), kc.to(dev), vc.to(dev), seq.to(dev)
+    run = lambda tbl, **kw: gqa_decode_paged_fn(d_q, d_kc, d_vc, tbl.to(dev), d_seq,  # noqa: E731
+                                                split_tokens=split, **kw)
+    out_shared = run(shared, shared_prefix_tokens=prefix, kv_reuse=True)
+    out_private = run(private, shared_prefix_tokens=prefix)
+    assert_decode_close(out_shared, ref)
+    assert_decode_close(out_shared, run(shared))
+    assert torch.equal(bits(out_shared), bits(out_private))
+    gate = (2 * torch.randn(len(suffix), 1, 24 * 256, generator=torch.Generator().manual_seed(9))
+            ).to(torch.bfloat16).to(dev)
+    gated = run(shared, shared_prefix_tokens=prefix, gate=gate)
+    from tileinfer_amd.kernels import fused_sigmoid_mul
+    assert torch.equal(bits(gated), bits(fused_sigmoid_mul(out_shared, gate.view_as(out_shared))))
+
+
+def test_shared_prefix_zero_and_whole_context(dev):
+    """shared_prefix_tokens=0 is the plain call (bitwise); a prefix that is some sequences' whole
+    context leaves the decode kernel nothing for them (the prefix part alone)."""
+    say("decode shared prefix edge cases")
+    q, kc, vc, shared, _, seq = _shared_prefix_step([0, 0, 200], 640, seed=5)
+    args = (q.to(dev), kc.to(dev), vc.to(dev), shared.to(dev), seq.to(dev))
+    plain = gqa_decode_paged_fn(*args)
+    assert torch.equal(bits(gqa_decode_paged_fn(*args, shared_prefix_tokens=0)), bits(plain))
+    assert_decode_close(gqa_decode_paged_fn(*args, shared_prefix_tokens=640),
+                        ref_gqa_decode_paged(q, kc, vc, shared, seq))
+    with pytest.raises(ValueError):
+        gqa_decode_paged_fn(*args, shared_prefix_tokens=100)        # not a page multiple
+    with pytest.raises(ValueError):
+        gqa_decode_paged_fn(*args, shared_prefix_tokens=640, variant="scalar")

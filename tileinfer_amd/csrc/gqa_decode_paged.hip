@@ -217,7 +217,20 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
   };
 
   auto store_out = [&](int b) {
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    // With a precomputed part (m_e, l_e, o_e): out = (w o + w_e o_e) / (w l + w_e l_e), weights
+    // 2^(m - M) and 2^(m_e - M), M the larger maximum.
+    float ws = 1.f, we = 0.f, l = l_tot;
+    const float* erow = nullptr;
+    if (a.pre_o) {  // uniform
+      const int64_t r = int64_t(b) * a.hq + h;
+      const float me = a.pre_ml[2 * r], le = a.pre_ml[2 * r + 1];
+      const float mm = fmaxf(m_run, me);
+      ws = m_run == -INFINITY ? 0.f : fast_exp2(m_run - mm);
+      we = me == -INFINITY ? 0.f : fast_exp2(me - mm);
+      l = ws * l_tot + we * le;
+      erow = a.pre_o + r * D;
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
     uint16_t* orow = a.out + (int64_t(b) * a.hq + h) * D;
     const uint16_t* grow = a.gate ? a.gate + b * a.gate_sb + int64_t(h) * a.gate_sh : nullptr;
 #pragma unroll
@@ -226,9 +239,20 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
       for (int r = 0; r < 4; ++r) {
         const int d = 128 * c + 32 * g + 8 * r;
         u32x4 w;
+        if (erow) {
+          const f32x4 e0 = *reinterpret_cast<const f32x4*>(erow + d);
+          const f32x4 e1 = *reinterpret_cast<const f32x4*>(erow + d + 4);
+          const float ev[8] = {e0[0], e0[1], e0[2], e0[3], e1[0], e1[1], e1[2], e1[3]};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          w[k] = pack2(o[8 * c + 2 * k][r] * inv, o[8 * c + 2 * k + 1][r] * inv, Tag{});
+          for (int k = 0; k < 4; ++k) {
+            w[k] = pack2((o[8 * c + 2 * k][r] * ws + ev[2 * k] * we) * inv,
+                         (o[8 * c + 2 * k + 1][r] * ws + ev[2 * k + 1] * we) * inv, Tag{});
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            w[k] = pack2(o[8 * c + 2 * k][r] * inv, o[8 * c + 2 * k + 1][r] * inv, Tag{});
+          }
         }
         if (grow) {
           const u32x4 gv = load16(grow + d);
@@ -363,9 +387,21 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
     slot0 = (int64_t(b) * a.hq + h) * a.max_splits;
   } else {
     const int nb = seq_tiles(a, b);
-    if (nb == 0) {
+    if (nb == 0) {  // no token of this kernel's range: zeros, or the precomputed part alone
+      float e[PER];
+      float inv = 0.f;
+      if (a.pre_o) {
+        const int64_t r = int64_t(b) * a.hq + h;
+        const float le = a.pre_ml[2 * r + 1];
+        inv = (a.pre_ml[2 * r] != -INFINITY && le > 0.f) ? 1.f / le : 0.f;
 #pragma unroll
-      for (int j = 0; j < PER; j += 2) put(j, 0u);
+        for (int q = 0; q < PER; ++q) e[q] = a.pre_o[r * D + d0 + q];
+      } else {
+#pragma unroll
+        for (int q = 0; q < PER; ++q) e[q] = 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < PER; j += 2) put(j, pack2(e[j] * inv, e[j + 1] * inv, Tag{}));
       return;
     }
     int tot = 0, pre = 0;
@@ -390,7 +426,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
   auto part = [&](int s) -> int64_t {
     return slot0 + s * stride + ((s == 0 && first_part_slot1) ? a.hq : 0);
   };
-  // Maximum over the parts' m, lane-parallel.
+  // Maximum over the parts' m (and the precomputed part's), lane-parallel.
   float m = -INFINITY;
   for (int s0 = 0; s0 < nparts; s0 += 64) {
     const int s = s0 + lane;
@@ -398,10 +434,19 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
   }
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+  const int64_t pr = int64_t(b) * a.hq + h;
+  const float me = a.pre_o ? a.pre_ml[2 * pr] : -INFINITY;
+  m = fmaxf(m, me);
   float acc[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) acc[j] = 0.f;
   float l = 0.f;
+  if (me != -INFINITY) {  // the precomputed part first (fixed order)
+    const float we = fast_exp2(me - m);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) acc[q] = we * a.pre_o[pr * D + d0 + q];
+    l = we * a.pre_ml[2 * pr + 1];
+  }
   if (m != -INFINITY) {
     // Parts in chunks of 64: lane s holds part s0+s's weight; the o rows of 8 parts are loaded
     // back to back so their latencies overlap. Summation order is fixed (ascending part).
@@ -599,7 +644,9 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
                  int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                  int32_t page_size, int64_t num_blocks, int32_t max_blocks_per_seq,
                  int32_t split_tokens, int32_t variant, int32_t dtype, const void* gate,
-                 int64_t gate_stride_b, int64_t gate_stride_h, void* stream) {
+                 int64_t gate_stride_b, int64_t gate_stride_h, void* stream,
+                 const float* pre_o = nullptr, const float* pre_ml = nullptr,
+                 int32_t prefix_tokens = 0) {
   if (dtype != TI_DTYPE_BF16 && dtype != TI_DTYPE_F16) {
     return fail(TI_EUNSUPPORTED, "ti_gqa_decode_paged: dtype code %d is not bf16/fp16", dtype);
   }
@@ -673,6 +720,12 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
   a.gate = static_cast<const uint16_t*>(gate);
   a.gate_sb = gate_stride_b;
   a.gate_sh = gate_stride_h;
+  a.pre_o = pre_o;
+  a.pre_ml = pre_ml;
+  a.ctx_offset = prefix_tokens;
+  if (pre_o != nullptr && kind == TI_DECODE_SCALAR) {
+    return fail(TI_EUNSUPPORTED, "ti_gqa_decode_paged_prefixed: MFMA variant only");
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf16 = dtype == TI_DTYPE_BF16;
   if (kind == TI_DECODE_SCALAR) {
@@ -732,4 +785,34 @@ extern "C" int ti_gqa_decode_paged_gated(
                           num_q_heads, num_kv_heads, head_dim, page_size, num_blocks,
                           max_blocks_per_seq, split_tokens, variant, dtype, gate, gate_stride_b,
                           gate_stride_h, stream);
+}
+
+extern "C" int ti_gqa_decode_paged_prefixed(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+    const void* v_cache, const int32_t* block_table, int64_t block_table_stride,
+    const int32_t* seqlen, void* out, void* workspace, int64_t workspace_bytes, int32_t batch,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+    int64_t num_blocks, int32_t max_blocks_per_seq, int32_t split_tokens, int32_t variant,
+    int32_t dtype, const void* gate, int64_t gate_stride_b, int64_t gate_stride_h,
+    const float* prefix_o, const float* prefix_ml, int32_t prefix_tokens, void* stream) {
+  using namespace ti;
+  if (batch > 0 && (prefix_o == nullptr || prefix_ml == nullptr)) {
+    return fail(TI_EINVAL, "ti_gqa_decode_paged_prefixed: null prefix part");
+  }
+  if (prefix_tokens < 0 || page_size <= 0 || prefix_tokens % page_size != 0 ||
+      prefix_tokens / page_size > max_blocks_per_seq) {
+    return fail(TI_EINVAL, "ti_gqa_decode_paged_prefixed: prefix_tokens %d must be a multiple of "
+                           "page_size within the table", prefix_tokens);
+  }
+  if ((reinterpret_cast<uintptr_t>(prefix_o) & 15) || (reinterpret_cast<uintptr_t>(prefix_ml) & 7)) {
+    return fail(TI_EINVAL, "ti_gqa_decode_paged_prefixed: prefix o 16-byte, (m, l) 8-byte aligned");
+  }
+  // The kernel covers tokens from prefix_tokens on: its table starts at that page.
+  const int32_t skip = prefix_tokens / page_size;
+  return decode_entry(q, q_stride_b, q_stride_h, k_cache, v_cache,
+                      block_table ? block_table + skip : nullptr, block_table_stride, seqlen, out,
+                      workspace, workspace_bytes, batch, num_q_heads, num_kv_heads, head_dim,
+                      page_size, num_blocks, max_blocks_per_seq - skip, split_tokens, variant,
+                      dtype, gate, gate_stride_b, gate_stride_h, stream, prefix_o, prefix_ml,
+                      prefix_tokens);
 }

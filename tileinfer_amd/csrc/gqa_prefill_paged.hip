@@ -56,6 +56,10 @@ struct PrefillArgs {
   // these strides; nullptr for the plain output.
   const uint16_t* gate;
   int64_t gate_st, gate_sh;
+  // Unnormalised output (instead of out): fp32 o relative to 2^m, [total_q][hq][D], and (m, l)
+  // [total_q][hq][2], m in exp2 units; nullptr for the normalised output.
+  float* uo;
+  float* uml;
 };
 
 constexpr float kRescaleSlack = 8.f;  // exp2 units a row maximum may rise before O is rescaled
@@ -684,6 +688,18 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       const int rho = wave * 16 * C + 16 * c + n;
       const int tok = rho / G;
       const int hh = rho - tok * G;
+      if (a.uo) {  // uniform: unnormalised rows for a later merge
+        const int64_t r = int64_t(sx.q_start + qb0 + tok) * a.hq + kvh * G + hh;
+#pragma unroll
+        for (int dt = 0; dt < NT; ++dt) {
+          *reinterpret_cast<f32x4*>(a.uo + r * D + 16 * dt + 4 * g) = o[c][dt];
+        }
+        if (g == 0) {
+          a.uml[2 * r] = m_run[c];
+          a.uml[2 * r + 1] = l_tot;
+        }
+        continue;
+      }
       uint16_t* orow =
           a.out + int64_t(sx.q_start + qb0 + tok) * a.o_st + int64_t(kvh * G + hh) * a.o_sh;
       const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -885,9 +901,20 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
   for (int j = 0; j < RPT; ++j) {
     const int r = r0 + j * (256 / TPR);
     if (r >= rows) break;
-    const float inv = l[j] > 0.f ? 1.f / l[j] : 0.f;
     const int tok = r / a.group;
     const int hh = r - tok * a.group;
+    if (a.uo) {  // unnormalised rows for a later merge
+      const int64_t ur = int64_t(sx.q_start + qb0 + tok) * a.hq + kvh * a.group + hh;
+      f32x4* dst = reinterpret_cast<f32x4*>(a.uo + ur * D + d0);
+      dst[0] = acc[j][0];
+      dst[1] = acc[j][1];
+      if (d0 == 0) {
+        a.uml[2 * ur] = m[j];
+        a.uml[2 * ur + 1] = l[j];
+      }
+      continue;
+    }
+    const float inv = l[j] > 0.f ? 1.f / l[j] : 0.f;
     uint16_t* orow = a.out + int64_t(sx.q_start + qb0 + tok) * a.o_st +
                      int64_t(kvh * a.group + hh) * a.o_sh + d0;
     u32x4 w;
@@ -1040,7 +1067,8 @@ int prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h, const v
                   int64_t workspace_bytes, int32_t batch, int32_t total_q, int32_t max_seqlen_q,
                   int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                   int64_t num_blocks, int32_t max_blocks_per_seq, int32_t causal, int32_t dtype,
-                  void* stream, const void* gate, int64_t gate_stride_t, int64_t gate_stride_h) {
+                  void* stream, const void* gate, int64_t gate_stride_t, int64_t gate_stride_h,
+                  float* uo = nullptr, float* uml = nullptr) {
   if (dtype != TI_DTYPE_BF16 && dtype != TI_DTYPE_F16) {
     return fail(TI_EUNSUPPORTED, "ti_gqa_prefill_paged: dtype code %d is not bf16/fp16", dtype);
   }
@@ -1062,7 +1090,8 @@ int prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h, const v
                 page_size);
   }
   if (batch == 0 || total_q == 0 || max_seqlen_q == 0) return TI_OK;
-  if (!q || !k_cache || !v_cache || !block_table || !cu_seqlens_q || !seqlen_k || !out) {
+  if (!q || !k_cache || !v_cache || !block_table || !cu_seqlens_q || !seqlen_k ||
+      (!out && !(uo && uml))) {
     return fail(TI_EINVAL, "ti_gqa_prefill_paged: null pointer");
   }
   if (block_table_stride < max_blocks_per_seq || q_stride_h % 8 || q_stride_t % 8 ||
@@ -1071,6 +1100,9 @@ int prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h, const v
       (reinterpret_cast<uintptr_t>(v_cache) & 15) ||
       (reinterpret_cast<uintptr_t>(workspace) & 255)) {
     return fail(TI_EINVAL, "ti_gqa_prefill_paged: rows must be 16-byte aligned (workspace 256)");
+  }
+  if ((reinterpret_cast<uintptr_t>(uo) & 15) || (reinterpret_cast<uintptr_t>(uml) & 7)) {
+    return fail(TI_EINVAL, "ti_gqa_prefill_paged_partial: o 16-byte, (m, l) 8-byte aligned");
   }
   if (gate && ((reinterpret_cast<uintptr_t>(gate) & 15) || gate_stride_t % 8 || gate_stride_h % 8)) {
     return fail(TI_EINVAL, "ti_gqa_prefill_paged_gated: gate rows must be 16-byte aligned");
@@ -1113,6 +1145,8 @@ int prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h, const v
   a.gate = static_cast<const uint16_t*>(gate);
   a.gate_st = gate_stride_t;
   a.gate_sh = gate_stride_h;
+  a.uo = uo;
+  a.uml = uml;
   if (balanced) {
     const int wgs = head_dim == 256 ? (bf16 ? balanced_wgs<256, Bf16>() : balanced_wgs<256, F16>())
                                     : (bf16 ? balanced_wgs<128, Bf16>() : balanced_wgs<128, F16>());
@@ -1185,4 +1219,22 @@ extern "C" int ti_gqa_prefill_paged_gated(
                            num_q_heads, num_kv_heads, head_dim, page_size, num_blocks,
                            max_blocks_per_seq, causal, dtype, stream, gate, gate_stride_t,
                            gate_stride_h);
+}
+
+extern "C" int ti_gqa_prefill_paged_partial(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+    const void* v_cache, const int32_t* block_table, int64_t block_table_stride,
+    const int32_t* cu_seqlens_q, const int32_t* seqlen_k, float* o_part, float* ml_part,
+    void* workspace, int64_t workspace_bytes, int32_t batch, int32_t total_q,
+    int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t page_size, int64_t num_blocks, int32_t max_blocks_per_seq, int32_t causal,
+    int32_t dtype, void* stream) {
+  if (!o_part || !ml_part) {
+    return ti::fail(TI_EINVAL, "ti_gqa_prefill_paged_partial: null output pointer");
+  }
+  return ti::prefill_paged(q, q_stride_t, q_stride_h, k_cache, v_cache, block_table,
+                           block_table_stride, cu_seqlens_q, seqlen_k, nullptr, 0, 0, workspace,
+                           workspace_bytes, batch, total_q, max_seqlen_q, num_q_heads,
+                           num_kv_heads, head_dim, page_size, num_blocks, max_blocks_per_seq,
+                           causal, dtype, stream, nullptr, 0, 0, o_part, ml_part);
 }

@@ -44,6 +44,19 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
     return s.value, m.value, w.value
 
 
+_STATIC_I32: dict = {}
+
+
+def _static_i32(values: tuple, dev: torch.device) -> torch.Tensor:
+    """A small int32 device tensor kept for reuse (made once per values/device, so that a call
+    captured in a graph does not create or upload it)."""
+    key = (values, str(dev))
+    t = _STATIC_I32.get(key)
+    if t is None:
+        t = _STATIC_I32[key] = torch.tensor(values, dtype=torch.int32, device=dev)
+    return t
+
+
 def _aligned_rows(t: torch.Tensor) -> bool:
     return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
             and all(s % 8 == 0 for s in t.stride()[:-1]))
@@ -62,6 +75,7 @@ def gqa_decode_paged_fn(
     variant: str = "auto",
     kv_reuse: bool = False,
     gate: torch.Tensor | None = None,
+    shared_prefix_tokens: int = 0,
 ) -> torch.Tensor:
     """Single-query paged GQA attention.
 
@@ -82,6 +96,14 @@ def gqa_decode_paged_fn(
             B * H_q * D values laid out [B, H_q, D] (``q_gate`` [B, 1, H_q * D] as the model has
             it): the output is ``decode * sigmoid(gate)``, applied in the kernel's epilogue —
             bitwise ``fused_sigmoid_mul(gqa_decode_paged_fn(...), gate)``.
+        shared_prefix_tokens: keyword-only P (a multiple of page_size, at most every seqlen_kv):
+            the caller's statement that the first P tokens of every sequence hold the same K/V
+            (prefix caching: shared blocks, or private copies of equal values). The prefix is then
+            attended once for the whole batch — all B x H_q queries against sequence 0's first P
+            tokens through the MFMA prefill kernel, unnormalised — and the decode kernel covers
+            tokens [P, seqlen) of each sequence and merges the two parts. Within the decode
+            tolerance of the plain call; bitwise the same for shared and private prefix pages.
+            MFMA variant only.
     Returns:
         [B, H_q, D] tensor in q's dtype.
     """
@@ -136,23 +158,52 @@ def gqa_decode_paged_fn(
     if b == 0:
         return out
     width = block_table.shape[1]
+    lib = _lib.load()
+    prefix = int(shared_prefix_tokens or 0)
+    if prefix:
+        if prefix < 0 or prefix % page_size or prefix // page_size > width:
+            raise ValueError(f"shared_prefix_tokens {prefix} must be a multiple of page_size "
+                             f"{page_size} within the block table's {width} pages")
+        if variant == "scalar":
+            raise ValueError("shared_prefix_tokens needs the MFMA variant")
+        from .gqa_prefill_paged import _workspace_bytes
+        pre_o = torch.empty((b, h_q, d), dtype=torch.float32, device=dev)
+        pre_ml = torch.empty((b, h_q, 2), dtype=torch.float32, device=dev)
+        pws_bytes = _workspace_bytes(1, b, h_q, h_kv, d, page_size, prefix // page_size)
+        pws = torch.empty(pws_bytes, dtype=torch.uint8, device=dev) if pws_bytes > 0 else None
+        # The batch's queries as the B "tokens" of one non-causal chunk over sequence 0's prefix.
+        _lib.check(lib.ti_gqa_prefill_paged_partial(
+            q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+            block_table.data_ptr(), block_table.stride(0), _static_i32((0, b), dev).data_ptr(),
+            _static_i32((prefix,), dev).data_ptr(), pre_o.data_ptr(), pre_ml.data_ptr(),
+            pws.data_ptr() if pws is not None else None, pws_bytes, 1, b, b, h_q, h_kv, d,
+            page_size, rows // page_size, prefix // page_size, 0, code, _lib.stream_handle(dev)))
+        width -= prefix // page_size
     _, _, ws_bytes = decode_plan(b, h_q, h_kv, d, page_size, width, split_tokens)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
-    lib = _lib.load()
+    table_width = block_table.shape[1]
     args = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
-            block_table.data_ptr(), block_table.stride(0) if width > 0 else 0,
+            block_table.data_ptr(), block_table.stride(0) if table_width > 0 else 0,
             seqlen_kv.data_ptr(), out.data_ptr(), ws.data_ptr() if ws is not None else None,
-            ws_bytes, b, h_q, h_kv, d, page_size, rows // page_size, width,
-            int(split_tokens or 0),
+            ws_bytes, b, h_q, h_kv, d, page_size, rows // page_size,
+            table_width if prefix else width, int(split_tokens or 0),
             _VARIANTS[variant] | (_lib.TI_DECODE_REUSE_KV if kv_reuse else 0), code)
+    g3 = None
+    if gate is not None:
+        if gate.numel() != b * h_q * d or gate.dtype != dt or gate.device != dev:
+            raise ValueError(f"gate must hold {b}x{h_q}x{d} values of q's dtype on q's device")
+        g3 = gate.reshape(b, h_q, d)
+        if not _aligned_rows(g3):
+            g3 = g3.contiguous()
+    if prefix:
+        _lib.check(lib.ti_gqa_decode_paged_prefixed(
+            *args, g3.data_ptr() if g3 is not None else None, g3.stride(0) if g3 is not None else 0,
+            g3.stride(1) if g3 is not None else 0, pre_o.data_ptr(), pre_ml.data_ptr(), prefix,
+            _lib.stream_handle(dev)))
+        return out
     if gate is None:
         _lib.check(lib.ti_gqa_decode_paged(*args, _lib.stream_handle(dev)))
         return out
-    if gate.numel() != b * h_q * d or gate.dtype != dt or gate.device != dev:
-        raise ValueError(f"gate must hold {b}x{h_q}x{d} values of q's dtype on q's device")
-    g3 = gate.reshape(b, h_q, d)
-    if not _aligned_rows(g3):
-        g3 = g3.contiguous()
     _lib.check(lib.ti_gqa_decode_paged_gated(*args, g3.data_ptr(), g3.stride(0), g3.stride(1),
                                              _lib.stream_handle(dev)))
     return out

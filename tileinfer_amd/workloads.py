@@ -202,7 +202,7 @@ def config5(seed: int = 1005, device="cpu", batch: int = 128, prefix: int = 8192
     return PagedStep(q=q, k_new=k_new, v_new=v_new, slot_mapping=decode_slots(table, ctx),
                      block_table=table, seqlen=torch.tensor(ctx, dtype=torch.int32, device=device),
                      k_cache=k_cache, v_cache=v_cache,
-                     meta={"seed": seed, "ctx": ctx, "shared": shared})
+                     meta={"seed": seed, "ctx": ctx, "shared": shared, "prefix_tokens": prefix})
 
 
 @dataclass
