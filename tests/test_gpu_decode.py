@@ -370,3 +370,33 @@ def test_shared_prefix_zero_and_whole_context(dev):
         gqa_decode_paged_fn(*args, shared_prefix_tokens=100)        # not a page multiple
     with pytest.raises(ValueError):
         gqa_decode_paged_fn(*args, shared_prefix_tokens=640, variant="scalar")
+
+
+def test_shared_prefix_graph_capture_replay(dev):
+    """The shared-prefix decode (prefix pass + suffix decode + merge) captured in a HIP graph after
+    a warm-up call: every replay matches the eager call bitwise."""
+    say("decode shared prefix graph capture")
+    q, kc, vc, shared, _, seq = _shared_prefix_step([300, 17, 900], 1024, seed=12)
+    q = q.to(dev)
+    args = (kc.to(dev), vc.to(dev), shared.to(dev), seq.to(dev))
+
+    def fn():
+        return gqa_decode_paged_fn(q, *args, kv_reuse=True, shared_prefix_tokens=1024)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = fn()
+    gen = torch.Generator(device=dev).manual_seed(4)
+    for r in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen, device=dev).to(q.dtype))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = fn()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(static_out), bits(eager)), f"replay {r}"
