@@ -178,6 +178,22 @@ def test_manager_shares_blocks_hint():
     assert m.shares_blocks([a, b]) and m.shares_blocks([b]) and not m.shares_blocks([c])
 
 
+def test_manager_common_prefix_tokens():
+    """The whole blocks every sequence of a batch holds in common (the shared_prefix_tokens of a
+    decode over it): 2 blocks for a and b, none once c joins, none for a single sequence."""
+    m = PagedKVManager(20, 16)
+    a = Sequence(list(range(40)))
+    m.admit(a)
+    m.finish_chunk(a, 32)
+    b = Sequence(list(range(32)) + [7] * 9)
+    m.admit(b)
+    c = Sequence([5] * 20)
+    m.admit(c)
+    assert m.common_prefix_tokens([a, b]) == 32
+    assert m.common_prefix_tokens([a, b, c]) == 0
+    assert m.common_prefix_tokens([a]) == 0
+
+
 def test_manager_full_prefix_match_leaves_a_token_to_prefill():
     m = PagedKVManager(10, 16)
     a = Sequence(list(range(32)))

@@ -142,6 +142,20 @@ class PagedKVManager:
             self.host_free.append(slot)
         return pairs
 
+    def common_prefix_tokens(self, seqs: list[Sequence]) -> int:
+        """Tokens at the start of every sequence held in the same physical blocks (whole blocks,
+        as prefix caching shares them): the ``shared_prefix_tokens`` of a decode over this batch.
+        0 for fewer than two sequences."""
+        if len(seqs) < 2:
+            return 0
+        n = min(len(s.block_table) for s in seqs)
+        first = seqs[0].block_table
+        common = 0
+        while common < n and first[common] >= 0 and all(s.block_table[common] == first[common]
+                                                         for s in seqs[1:]):
+            common += 1
+        return common * self.block_size
+
     def shares_blocks(self, seqs: list[Sequence]) -> bool:
         """Whether any block of these sequences is held by more than one sequence: the decode
         hint ``kv_reuse`` (shared pages are then worth keeping in cache)."""
