@@ -460,8 +460,9 @@ def run_config(cfg: int, args, dev) -> dict:
         # The prefix attended once for the batch (the caller's statement that every sequence
         # shares its first 8192 tokens), against the plain call's output.
         prefix = st.meta["prefix_tokens"]
+        # (The suffixes are each sequence's own pages, read once: the streaming cache policy.)
         shared_fn = lambda: gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen,  # noqa: E731
-                                                 kv_reuse=True, shared_prefix_tokens=prefix)
+                                                 shared_prefix_tokens=prefix)
         shared_us = _time(shared_fn, args.steps, args.warmup)
         plain = gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen, kv_reuse=True)
         shared_err = float((shared_fn().float() - plain.float()).abs().max())
