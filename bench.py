@@ -404,6 +404,72 @@ def prefill_config4(st, chunk_slots, kc, vc, dev, args) -> dict:
             "peak_TFLOPs_bf16_dense": 2500.0}
 
 
+def config_parity(cfg: int, st, key, val, slots, out, dev) -> dict:
+    """Parity on the run itself: appended rows bit-exact; the decode output of every sequence
+    against the CPU oracle (max abs error; max relative error over outputs with |ref| >= 0.05;
+    the largest fraction of atol 2e-2 + rtol 1e-2 · |ref| used); for config 5 the shared and
+    the private prefix layout bitwise equal (plain call and shared-prefix call)."""
+    from oracle.ref_torch import ref_gqa_decode_paged
+    from tileinfer_amd import workloads as wl
+
+    rows = lambda c: c.view(-1, HKV * HEAD_DIM)  # noqa: E731
+    live = slots >= 0
+    sl = slots[live].long()
+    append_ok = all(torch.equal(rows(c)[sl].view(torch.int16),
+                                x.reshape(-1, HKV * HEAD_DIM)[live].view(torch.int16))
+                    for c, x in ((st.k_cache, key), (st.v_cache, val)))
+    ref = ref_gqa_decode_paged(st.q.cpu(), st.k_cache.cpu(), st.v_cache.cpu(),
+                               st.block_table.cpu(), st.seqlen.cpu(), BLOCK).float()
+    err = (out.float().cpu() - ref).abs()
+    big = ref.abs() >= 0.05
+    res = {"append_bit_exact": append_ok,
+           "decode_max_abs_err": round(float(err.max()), 6),
+           "decode_max_rel_err": round(float((err[big] / ref[big].abs()).max()), 6)
+           if bool(big.any()) else None,
+           "decode_tol_used": round(float((err / (2e-2 + 1e-2 * ref.abs())).max()), 4),
+           "decode_within_tol": bool((err <= 2e-2 + 1e-2 * ref.abs()).all()),
+           "sequences_checked": int(st.seqlen.numel())}
+    if cfg == 5:
+        pv = wl.config5(device=dev, shared=False)  # same values, every prefix block a private copy
+        store_kvcache(pv.k_new, pv.v_new, rows(pv.k_cache), rows(pv.v_cache), pv.slot_mapping)
+        bits = lambda t: t.view(torch.int16)  # noqa: E731
+        priv = gqa_decode_paged_fn(pv.q, pv.k_cache, pv.v_cache, pv.block_table, pv.seqlen,
+                                   kv_reuse=True)
+        res["shared_vs_private_bitwise"] = bool(torch.equal(bits(out), bits(priv)))
+        prefix = st.meta["prefix_tokens"]
+        a = gqa_decode_paged_fn(st.q, st.k_cache, st.v_cache, st.block_table, st.seqlen,
+                                shared_prefix_tokens=prefix)
+        b = gqa_decode_paged_fn(pv.q, pv.k_cache, pv.v_cache, pv.block_table, pv.seqlen,
+                                shared_prefix_tokens=prefix)
+        res["shared_vs_private_bitwise_shared_prefix_call"] = bool(torch.equal(bits(a), bits(b)))
+        del pv, priv, a, b
+    return res
+
+
+def config_cpu_reference(st, key, val, slots) -> dict:
+    """The CPU oracle (append + decode of the reference recipe) over the whole layer on the host
+    cores: 1 warm-up, then the median of 3 runs."""
+    from oracle.ref_torch import ref_gqa_decode_paged, ref_store_kvcache
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    kc, vc = st.k_cache.cpu(), st.v_cache.cpu()
+    k, v, sl = key.cpu(), val.cpu(), slots.cpu()
+    q, tb, sq = st.q.cpu(), st.block_table.cpu(), st.seqlen.cpu()
+
+    def run():
+        t0 = time.perf_counter()
+        ref_store_kvcache(k, v, kc.view(-1, HKV * HEAD_DIM), vc.view(-1, HKV * HEAD_DIM), sl)
+        ref_gqa_decode_paged(q, kc, vc, tb, sq, BLOCK)
+        return time.perf_counter() - t0
+
+    run()
+    t = statistics.median([run() for _ in range(3)])
+    return {"us_per_layer_step": round(t * 1e6, 1), "cores": cores, "kind": "port",
+            "sample": f"the whole layer ({sq.numel()} sequences), append + decode by the CPU "
+                      f"oracle (oracle/ref_torch.py), median of 3 after 1 warm-up"}
+
+
 def run_config(cfg: int, args, dev) -> dict:
     """One attention layer of BASELINE config 1, 2, 4 or 5 (append, then decode), on the GPU."""
     from tileinfer_amd import workloads as wl
@@ -436,6 +502,13 @@ def run_config(cfg: int, args, dev) -> dict:
                  args.steps, args.warmup)
     a_bytes = append_bytes(slots, HKV * HEAD_DIM)
     d_bytes = decode_bytes(ctx)
+    # Parity and the CPU reference on this state (the timed append, then decode), before the
+    # extra measurements below write elsewhere in the pool.
+    out = gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen,
+                              split_tokens=args.split_tokens, variant=args.variant, kv_reuse=reuse)
+    checks = {"parity": config_parity(cfg, st, key, val, slots, out, dev)}
+    if not args.no_cpu_baseline:
+        checks["cpu_reference"] = config_cpu_reference(st, key, val, slots)
     if cfg == 4:
         # Also as two calls (chunk, then the 32 decode tokens), and a bulk append rate.
         two = _time(lambda: (store_kvcache(st.meta["chunk_k"], st.meta["chunk_v"], rows(kc),
@@ -489,7 +562,7 @@ def run_config(cfg: int, args, dev) -> dict:
         "decode_us": round(d_us, 2), "decode_GBps_algorithmic": round(d_bytes / (d_us * 1e-6) / 1e9, 1),
         "decode_pct_of_peak_hbm": round(100 * d_bytes / (d_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 2),
         "append_us": round(a_us, 2), "append_GBps_algorithmic": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
-        "us_per_layer_step": round(a_us + d_us, 2), **extra,
+        "us_per_layer_step": round(a_us + d_us, 2), **extra, **checks,
     }
 
 
