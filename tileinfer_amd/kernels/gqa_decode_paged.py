@@ -49,7 +49,8 @@ _STATIC_I32: dict = {}
 
 def _static_i32(values: tuple, dev: torch.device) -> torch.Tensor:
     """A small int32 device tensor kept for reuse (made once per values/device, so that a call
-    captured in a graph does not create or upload it)."""
+    captured in a graph does not create or upload it). Entries are never evicted: a captured
+    graph holds their addresses, and there is one per (batch size, prefix length) in use."""
     key = (values, str(dev))
     t = _STATIC_I32.get(key)
     if t is None:
