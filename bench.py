@@ -594,7 +594,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}): "
-              "this build has no multi-GPU path; the sharding design is described in DESIGN.md.",
+              "this build has no multi-GPU path (the path would shard by KV head or by sequence, "
+              "neither of which exchanges K/V between GPUs).",
               file=sys.stderr)
         sys.exit(2)
 
