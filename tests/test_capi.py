@@ -108,6 +108,23 @@ def test_python_wrappers_validate_before_launch():
         gqa_prefill_paged_fn(q, kc, kc, bt, cu, sl, 1)
 
 
+def test_qknorm_rope_append_rejects_bad_q_out():
+    """A caller-supplied q_out of the wrong shape or dtype is refused before anything runs (the
+    kernel would otherwise write q rows past its end)."""
+    from tileinfer_amd.kernels.qknorm_rope import qknorm_rope_append
+    q = torch.zeros(3, 24, 256, dtype=torch.bfloat16)
+    k = torch.zeros(3, 4, 256, dtype=torch.bfloat16)
+    w = torch.zeros(256, dtype=torch.bfloat16)
+    cs = torch.zeros(64, dtype=torch.bfloat16)
+    cache = torch.zeros(64, 1024, dtype=torch.bfloat16)
+    slots = torch.zeros(3, dtype=torch.int32)
+    for bad in (torch.zeros(2, 24, 256, dtype=torch.bfloat16),   # too few rows
+                torch.zeros(3, 24, 256, dtype=torch.float16),    # wrong dtype
+                torch.zeros(3, 24, 512, dtype=torch.bfloat16)[:, :, ::2]):  # strided rows
+        with pytest.raises(ValueError, match="q_out"):
+            qknorm_rope_append(q, k, k, w, w, cs, cs, cache, cache, slots, q_out=bad)
+
+
 def _prefill_abi(batch=1, total_q=4, max_q=4, hq=24, hkv=4, d=256, ps=16, dtype=0, ptr=None):
     lib = _lib.load()
     return lib.ti_gqa_prefill_paged(ptr, 24 * d, d, ptr, ptr, ptr, 8, ptr, ptr, ptr, 24 * d, d,

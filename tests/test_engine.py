@@ -7,7 +7,7 @@ reused last-in first-out, and deallocation walks a table in reverse (engine/bloc
 import numpy as np
 import pytest
 import torch
-from hypothesis import given, settings
+from hypothesis import example, given, settings
 from hypothesis import strategies as st
 
 from tileinfer_amd.engine import (AttentionContext, BlockManager, PagedKVManager, PrefixCache,
@@ -292,6 +292,23 @@ def test_kv_cache_layout_views():
     assert kl.num_blocks_for_budget(2 * 16 * 4 * 8 * 2 * 3 * 10 + 5, 16, 4, 8, 3) == 10
 
 
+def test_pool_sizing_from_free_memory():
+    """The runner's sizing (engine/model_runner.py:218-256): budget = total·util − used − other
+    pools; blocks = budget // bytes per block id over K, V and every attention layer (at least 1);
+    the table width is max_model_len // 16 + 2, clamped to the pool."""
+    gib = 2**30
+    # 288 GiB card, 20 GiB in use (weights), 90 % target, 4 GiB of other pools.
+    budget = kl.kv_budget(288 * gib, 268 * gib, 0.9, reserved_bytes=4 * gib)
+    assert budget == int(288 * gib * 0.9) - 20 * gib - 4 * gib
+    per_block = 2 * 16 * 4 * 256 * 2 * 16                  # K+V x 16 rows x 4 heads x 256 x bf16 x 16 layers
+    assert kl.block_bytes(16, 4, 256, 16) == per_block == 1 << 20
+    nb = kl.num_blocks_for_budget(budget, 16, 4, 256, 16)
+    assert nb == budget // per_block and nb == 240_844    # 235.2 GiB of 1 MiB blocks
+    assert kl.num_blocks_for_budget(-5, 16, 4, 256, 16) == 1
+    assert kl.max_blocks_per_seq(262_144, 16, nb) == 16_386
+    assert kl.max_blocks_per_seq(262_144, 16, 1000) == 1000
+
+
 def test_attention_context_is_thread_local():
     import threading
     ctx = AttentionContext()
@@ -340,3 +357,93 @@ def test_swap_pool_exhaustion_and_free_while_swapped():
     assert m.swap_out(a, max_blocks=1) == [(0, 0)]
     m.free(a)                                    # freeing a swapped sequence returns its host slot
     assert m.host_free == [0] and m.block_manager.num_free_blocks == 10
+
+
+# ----------------------------------------------------------------------------- prefix index: races
+
+
+def test_identical_prompts_recorded_twice_never_share_foreign_blocks():
+    """Two identical prompts admitted before either is recorded compute the same prefix into
+    different blocks. After both are recorded and the second is freed, a third copy may share only
+    blocks that still hold that prefix -- never blocks that now belong to another sequence."""
+    m = PagedKVManager(12, 16)
+    prompt = list(range(40))
+    a, b = Sequence(prompt), Sequence(prompt)
+    assert m.admit(a) and m.admit(b)
+    assert a.block_table == [0, 1, 2] and b.block_table == [3, 4, 5]
+    m.finish_chunk(a, 32)                       # two whole blocks of each are recorded
+    m.finish_chunk(b, 32)
+    m.free(b)                                   # frees 5, 4, 3 (3 on top of the stack)
+    d = Sequence([7] * 40)
+    assert m.admit(d)
+    assert d.block_table == [3, 4, 5]           # the unrelated sequence now owns b's old blocks
+    c = Sequence(prompt + [99])
+    assert m.admit(c)
+    shared = c.block_table[:c.num_cached_tokens // 16]
+    assert c.num_cached_tokens == 32 and shared == [0, 1]
+    assert not set(shared) & set(d.block_table)
+    refs = m.block_manager.ref_counts
+    assert refs[0] == 2 and refs[1] == 2 and refs[3] == 1
+
+
+def test_prefix_index_evicts_exactly_the_freed_chains():
+    """A boundary recorded under the first block that computed it keeps that block; freeing the
+    sequence that holds it forgets it (and everything below), freeing the duplicate does not."""
+    pc = PrefixCache(2)
+    pc.add([1, 2, 3, 4], [10, 11])
+    pc.add([1, 2, 3, 4, 5, 6], [20, 21, 22])   # same first two boundaries: kept as 10, 11
+    assert pc.find_longest_prefix([1, 2, 3, 4, 5, 6]) == ([10, 11, 22], 6)
+    pc.evict_block(21)                          # names no entry: nothing forgotten
+    assert pc.num_entries == 3
+    pc.evict_block(11)                          # [10, 11] and [10, 11, 22] go
+    assert pc.find_longest_prefix([1, 2, 3, 4, 5, 6]) == ([10], 2)
+    assert pc.num_entries == 1
+    pc.add([1, 2, 3, 4], [10, 30])
+    assert pc.find_longest_prefix([1, 2, 3, 4]) == ([10, 30], 4)
+
+
+@settings(max_examples=300, deadline=None)
+@given(st.lists(st.tuples(st.sampled_from(["admit", "finish", "decode", "free"]),
+                          st.integers(0, 3), st.integers(5, 14)), max_size=50))
+# The race that needs a careful index: two copies of one prompt computed into different blocks,
+# both recorded, the second freed and its blocks taken by another prompt, then a third copy.
+@example([("admit", 0, 14), ("admit", 2, 14), ("finish", 0, 5), ("finish", 2, 5),
+          ("free", 2, 5), ("admit", 1, 14), ("admit", 2, 14)])
+def test_shared_blocks_always_hold_the_shared_tokens(ops):
+    """Whatever the interleaving of admissions, recordings and frees, a prefix hit shares only
+    blocks whose recorded tokens are the new sequence's tokens at the same positions: every block
+    of a live table is tagged with the (position, tokens) it holds, and a shared block's tag must
+    match."""
+    Sequence.block_size = 4                 # the fixture restores 16
+    m = PagedKVManager(24, 4)
+    prompts = [[1] * 14, [3] * 14, [1] * 8 + [2] * 6]
+    live: dict[int, Sequence] = {}
+    tag: dict[int, tuple] = {}              # block -> (logical index, tokens) it holds
+    for op, k, n in ops:
+        if op == "admit" and k not in live:
+            s = Sequence(prompts[k % 2 if k < 3 else 2][:n])
+            if m.admit(s):
+                for i, bid in enumerate(s.block_table[:s.num_cached_tokens // 4]):
+                    assert tag[bid] == (i, tuple(s.token_ids[4 * i:4 * i + 4])), (bid, tag[bid])
+                for i in range(s.num_cached_tokens // 4, len(s.block_table)):
+                    tag[s.block_table[i]] = (i, tuple(s.token_ids[4 * i:4 * i + 4]))
+                live[k] = s
+        elif op == "finish" and k in live and live[k].is_prefill:
+            s = live[k]
+            whole = s.num_tokens // 4 * 4 - s.num_cached_tokens    # whole blocks first: recorded
+            if whole > 0:
+                m.finish_chunk(s, whole)
+            if s.num_tokens > s.num_cached_tokens:
+                m.finish_chunk(s, s.num_tokens - s.num_cached_tokens)
+            s.is_prefill = False
+        elif op == "decode" and k in live and not live[k].is_prefill:
+            s = live[k]
+            s.append_token(n % 3)
+            if not m.can_append(s):
+                m.free(live.pop(k))
+                continue
+            m.append_slot(s)
+            i = (len(s) - 1) // 4
+            tag[s.block_table[i]] = (i, tuple(s.token_ids[4 * i:4 * i + 4]))
+        elif op == "free" and k in live:
+            m.free(live.pop(k))

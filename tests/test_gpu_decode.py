@@ -48,11 +48,12 @@ def test_config2_vs_oracle(variant, dev):
 
 @pytest.mark.parametrize("variant", VARIANTS)
 def test_reference_selftest_shape(variant, dev):
-    """kernels/gqa_decode_paged.py:481-512 at reduced batch: Hq 32, Hkv 8, D 128, seqlen 8192,
-    a fifth of the batch shortened to U[2048, 8192), every sequence on the same sequential table."""
+    """kernels/gqa_decode_paged.py:472-512 at its default batch: B 32, Hq 32, Hkv 8, D 128,
+    seqlen 8192, a fifth of the batch shortened to U[2048, 8192), every sequence on the same
+    sequential table."""
     say(f"decode reference selftest shape variant={variant}")
     g = torch.Generator().manual_seed(0)
-    b, hq, hkv, d, seqlen, ps = 10, 32, 8, 128, 8192, 16
+    b, hq, hkv, d, seqlen, ps = 32, 32, 8, 128, 8192, 16
     max_pages = int(seqlen * 1.1) // ps
     seq = torch.full((b,), seqlen, dtype=torch.int32)
     seq[: b // 5] = torch.randint(seqlen // 4, seqlen, (b // 5,), generator=g, dtype=torch.int32)

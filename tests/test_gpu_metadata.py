@@ -1,6 +1,7 @@
 """DeviceBlockTables (ti_paged_metadata) against the host builders over a simulated serving run:
 admissions with prefix hits, prefill chunks, decode steps that cross block boundaries, finished
-sequences whose rows are reused, swap-out / swap-in with ``invalidate``, graph padding."""
+sequences whose rows are reused, swap-out / swap-in and re-admission (new table generations),
+graph padding."""
 import random
 
 import numpy as np
@@ -70,8 +71,7 @@ def test_serving_run_matches_host_builders(dev):
         if parked and rng.random() < 0.2:
             s = parked.pop(0)
             if m.can_swap_in(s):
-                m.swap_in(s)
-                dt.invalidate(s)                # new ids at old positions
+                m.swap_in(s)                    # new ids at old positions: a new generation
                 live.append(s)
             else:
                 parked.append(s)
@@ -141,3 +141,29 @@ def test_metadata_feeds_the_kernels(dev):
         store_kvcache(kn, kn, k2.view(-1, 1024), v2.view(-1, 1024), slots)
         outs.append(gqa_decode_paged_fn(q, k2, v2, tables, ctx))
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
+def test_readmitted_sequence_resends_its_table(dev):
+    """Recompute preemption: a sequence is freed (its row kept: no ``release``), its blocks go to
+    another sequence, and it is admitted again into other blocks. The next step must send the new
+    table whole, not only the entries past the old count."""
+    say("device metadata: free and re-admit without release")
+    m = PagedKVManager(64, BS, enable_prefix_caching=False)
+    dt = DeviceBlockTables(max_seqs=4, max_blocks_per_seq=16, block_size=BS, device=dev)
+    a = Sequence(list(range(40)))                 # blocks 0, 1, 2
+    assert m.admit(a)
+    m.finish_chunk(a, a.num_tokens)
+    a.is_prefill = False
+    a.append_token(1)
+    m.append_slot(a)
+    check_decode(dt, [a])
+    m.free(a)                                     # 2, 1, 0 back on the free stack
+    b = Sequence(list(range(100, 120)))          # takes 0, 1
+    assert m.admit(b)
+    a.num_cached_tokens = 0
+    assert m.admit(a) and a.block_table == [2, 3, 4]
+    m.finish_chunk(a, a.num_tokens)
+    a.append_token(2)
+    m.append_slot(a)                              # 42 tokens: 3 blocks, as before the free
+    check_decode(dt, [a, b])
+    assert dt.block_tables[0, :3].tolist() == [2, 3, 4]

@@ -221,7 +221,9 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     // 2^(m - M) and 2^(m_e - M), M the larger maximum.
     float ws = 1.f, we = 0.f, l = l_tot;
     const float* erow = nullptr;
-    if (a.pre_o) {  // uniform
+    // A row shorter than the shared prefix (the runner's graph-padding rows: context 1, no
+    // pages) is outside the prefix contract and gets no prefix part: zeros, as plain decode.
+    if (a.pre_o && a.seqlen[b] >= a.ctx_offset) {  // uniform
       const int64_t r = int64_t(b) * a.hq + h;
       const float me = a.pre_ml[2 * r], le = a.pre_ml[2 * r + 1];
       const float mm = fmaxf(m_run, me);
@@ -390,7 +392,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
     if (nb == 0) {  // no token of this kernel's range: zeros, or the precomputed part alone
       float e[PER];
       float inv = 0.f;
-      if (a.pre_o) {
+      if (a.pre_o && a.seqlen[b] >= a.ctx_offset) {  // shorter rows: zeros (see store_out)
         const int64_t r = int64_t(b) * a.hq + h;
         const float le = a.pre_ml[2 * r + 1];
         inv = (a.pre_ml[2 * r] != -INFINITY && le > 0.f) ? 1.f / le : 0.f;

@@ -14,8 +14,11 @@ reference's graph-padding rows (slot -1, context length 1, block -1; engine/mode
 524-527). The outputs are views of static device buffers, so a captured decode graph can read
 them in place.
 
-A table changed other than by appending (swap-in assigns new ids to old positions) must be
-announced with ``invalidate(seq)``; ``release(seq)`` frees the row of a finished sequence.
+A table replaced or changed other than by appending (freed and re-admitted, swapped out or in) is
+re-sent whole: the block manager and ``PagedKVManager`` bump ``Sequence.table_generation`` when
+they do that, and a step compares it with the generation it last sent. Code that edits a table
+by hand calls ``seq.table_changed()`` (or ``invalidate(seq)``); ``release(seq)`` frees the row of
+a finished sequence.
 """
 from __future__ import annotations
 
@@ -39,8 +42,9 @@ class DeviceBlockTables:
         self.tables = torch.full((max_seqs, max_blocks_per_seq), -1, dtype=torch.int32,
                                  device=self.device)
         self._free_rows = list(range(max_seqs - 1, -1, -1))
-        self._row: dict[int, int] = {}    # seq_id -> persistent row
-        self._sent: dict[int, int] = {}   # seq_id -> table entries already on the device
+        # seq_id -> [persistent row, table entries already on the device, table generation they
+        # belong to]; a new generation (the table was replaced or edited) re-sends the table.
+        self._state: dict[int, list] = {}
         # Static outputs (a captured graph reads these in place).
         self.slot_mapping = torch.full((self.max_tokens + self.max_batch,), -1, dtype=torch.int32,
                                        device=self.device)
@@ -50,7 +54,9 @@ class DeviceBlockTables:
         # Packed per-step input: host staging (pinned, two alternating buffers) and device copy.
         self._cap = 0
         self._host: list[torch.Tensor] = []
-        self._events: list[torch.cuda.Event | None] = []
+        self._host_np: list[np.ndarray] = []
+        self._events: list[torch.cuda.Event] = []
+        self._recorded: list[bool] = []
         self._dev: torch.Tensor | None = None
         self._flip = 0
         self.last_upload_words = 0  # int32 words the last step sent to the device
@@ -58,29 +64,27 @@ class DeviceBlockTables:
     # -- rows --------------------------------------------------------------------------------------
 
     def row_of(self, seq: Sequence) -> int:
-        return self._row[seq.seq_id]
+        return self._state[seq.seq_id][0]
 
     def release(self, seq: Sequence) -> None:
         """Free the sequence's row (its device contents are overwritten by the next owner)."""
-        row = self._row.pop(seq.seq_id, None)
-        self._sent.pop(seq.seq_id, None)
-        if row is not None:
-            self._free_rows.append(row)
+        st = self._state.pop(seq.seq_id, None)
+        if st is not None:
+            self._free_rows.append(st[0])
 
     def invalidate(self, seq: Sequence) -> None:
-        """Re-upload the sequence's whole table at the next step (after an in-place change)."""
-        if seq.seq_id in self._sent:
-            self._sent[seq.seq_id] = 0
+        """Re-upload the sequence's whole table at the next step (after an in-place change that
+        did not go through ``Sequence.table_changed``)."""
+        st = self._state.get(seq.seq_id)
+        if st is not None:
+            st[1] = 0
 
-    def _ensure_row(self, seq: Sequence) -> int:
-        row = self._row.get(seq.seq_id)
-        if row is None:
-            if not self._free_rows:
-                raise RuntimeError("DeviceBlockTables: no free row (raise max_seqs)")
-            row = self._free_rows.pop()
-            self._row[seq.seq_id] = row
-            self._sent[seq.seq_id] = 0
-        return row
+    def _new_row(self, seq: Sequence) -> list:
+        if not self._free_rows:
+            raise RuntimeError("DeviceBlockTables: no free row (raise max_seqs)")
+        st = [self._free_rows.pop(), 0, seq.table_generation]
+        self._state[seq.seq_id] = st
+        return st
 
     # -- one step ----------------------------------------------------------------------------------
 
@@ -90,12 +94,13 @@ class DeviceBlockTables:
             pin = self.device.type == "cuda"
             self._host = [torch.empty(self._cap, dtype=torch.int32, pin_memory=pin)
                           for _ in range(2)]
-            self._events = [None, None]
+            self._host_np = [h.numpy() for h in self._host]
+            self._events = [torch.cuda.Event(), torch.cuda.Event()]
+            self._recorded = [False, False]
             self._dev = torch.empty(self._cap, dtype=torch.int32, device=self.device)
         self._flip ^= 1
-        ev = self._events[self._flip]
-        if ev is not None:
-            ev.synchronize()  # the copy that last read this staging buffer has finished
+        if self._recorded[self._flip]:
+            self._events[self._flip].synchronize()  # the copy that last read this buffer is done
         return self._host[self._flip], self._dev
 
     def step(self, seqs: list[Sequence], new_tokens: list[int] | None = None,
@@ -128,33 +133,41 @@ class DeviceBlockTables:
             raise ValueError(f"pad_to {pad_to} outside [{n}, {self.max_batch}]")
         if len(ntok) != n:
             raise ValueError("new_tokens must have one entry per sequence")
-        bs = self.block_size
-        rows = np.empty(n, dtype=np.int32)
+        state = self._state
+        rows: list[int] = []
+        tlen: list[int] = []
+        upd_off = [0]
         upd_cols: list[int] = []
         upd_ids: list[int] = []
-        upd_off = np.zeros(n + 1, dtype=np.int32)
-        tlen = np.empty(n, dtype=np.int32)
-        need_w = 0
-        for i, s in enumerate(seqs):
-            rows[i] = self._ensure_row(s)
+        sent_now: list[tuple[list, int, int]] = []  # committed once the upload is enqueued
+        for s in seqs:
             table = s.block_table
-            sent = self._sent[s.seq_id]
-            if len(table) > self.max_blocks:
-                raise ValueError(f"sequence {s.seq_id}: {len(table)} blocks > {self.max_blocks}")
-            if len(table) > sent:
-                upd_cols.extend(range(sent, len(table)))
+            k = len(table)
+            st = state.get(s.seq_id)
+            if st is None:
+                st = self._new_row(s)
+            gen = s.table_generation
+            sent = st[1] if st[2] == gen else 0
+            if k > sent:  # ids appended since the last step (all of them for a new generation)
+                if k > self.max_blocks:
+                    raise ValueError(f"sequence {s.seq_id}: {k} blocks > {self.max_blocks}")
+                upd_cols.extend(range(sent, k))
                 upd_ids.extend(table[sent:])
-                self._sent[s.seq_id] = len(table)
-            upd_off[i + 1] = len(upd_cols)
-            tlen[i] = len(table)
-            need_w = max(need_w, len(table))
-        tok_off = np.zeros(n + 1, dtype=np.int32)
-        if n:
-            tok_off[1:] = np.cumsum(np.asarray(ntok, dtype=np.int64))
-        total_tok = int(tok_off[-1])
+                sent_now.append((st, k, gen))
+            elif k < sent:  # shrunk without a new generation: re-send what is left
+                upd_cols.extend(range(k))
+                upd_ids.extend(table)
+                sent_now.append((st, k, gen))
+            rows.append(st[0])
+            tlen.append(k)
+            upd_off.append(len(upd_cols))
+        tok_off = [0]
+        for t in ntok:
+            tok_off.append(tok_off[-1] + int(t))
+        total_tok = tok_off[-1]
         if total_tok + (pad - n) > self.slot_mapping.numel():
             raise ValueError(f"{total_tok} tokens exceed max_tokens={self.max_tokens}")
-        w = need_w if width is None else int(width)
+        w = max(tlen, default=0) if width is None else int(width)
         if w > self.max_blocks or w < 0:
             raise ValueError(f"width {w} outside [0, {self.max_blocks}]")
         u = len(upd_cols)
@@ -166,28 +179,22 @@ class DeviceBlockTables:
         words = o_id + u
         self.last_upload_words = words
         host, dev = self._staging(words)
-        h = host.numpy()
-        h[0:n] = rows
-        h[o_ctx:o_len] = ctx
-        h[o_len:o_tok] = tlen
-        h[o_tok:o_upd] = tok_off
-        h[o_upd:o_col] = upd_off
-        if u:
-            h[o_col:o_id] = upd_cols
-            h[o_id:words] = upd_ids
+        h = self._host_np[self._flip]
+        h[:words] = np.fromiter(
+            (x for part in (rows, ctx, tlen, tok_off, upd_off, upd_cols, upd_ids) for x in part),
+            dtype=np.int32, count=words)
         stream = torch.cuda.current_stream(self.device)
         dev[:words].copy_(host[:words], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record(stream)
-        self._events[self._flip] = ev
+        self._events[self._flip].record(stream)
+        self._recorded[self._flip] = True
         base = dev.data_ptr()
-        at = lambda k: base + 4 * k  # noqa: E731
-        lib = _lib.load()
-        _lib.check(lib.ti_paged_metadata(
+        _lib.check(_lib.load().ti_paged_metadata(
             self.tables.data_ptr(), self.tables.stride(0), self.tables.shape[0], self.max_blocks,
-            at(0), at(o_ctx), at(o_len), at(o_tok), at(o_upd), at(o_col), at(o_id),
-            n, pad, self.slot_mapping.data_ptr(), self.context_lens.data_ptr(),
-            self.block_tables.data_ptr(), self.block_tables.stride(0), w, bs,
-            stream.cuda_stream))
+            base, base + 4 * o_ctx, base + 4 * o_len, base + 4 * o_tok, base + 4 * o_upd,
+            base + 4 * o_col, base + 4 * o_id, n, pad, self.slot_mapping.data_ptr(),
+            self.context_lens.data_ptr(), self.block_tables.data_ptr(),
+            self.block_tables.stride(0), w, self.block_size, stream.cuda_stream))
+        for st, k, gen in sent_now:
+            st[1], st[2] = k, gen
         return (self.slot_mapping[:total_tok + pad - n], self.block_tables[:pad, :w],
                 self.context_lens[:pad])

@@ -46,6 +46,29 @@ def num_blocks_for_budget(budget_bytes: int, block_size: int, num_kv_heads: int,
                                                     num_layers, dtype))
 
 
+def kv_budget(total_bytes: int, free_bytes: int, gpu_memory_utilization: float,
+              reserved_bytes: int = 0) -> int:
+    """Bytes the cache slab may take: ``total · utilization − used − reserved``, with
+    ``used = total − free`` measured before the slab exists and ``reserved`` the other pools the
+    runner sizes from the same budget (its recurrent-state pools; engine/model_runner.py:218-221,
+    249-250). May be negative when memory is already over the utilisation target."""
+    used = int(total_bytes) - int(free_bytes)
+    return int(int(total_bytes) * gpu_memory_utilization) - used - int(reserved_bytes)
+
+
+def kv_budget_from_device(gpu_memory_utilization: float, reserved_bytes: int = 0,
+                          device: torch.device | str | None = None) -> int:
+    """``kv_budget`` with the device's current free and total memory (``torch.cuda.mem_get_info``)."""
+    free, total = torch.cuda.mem_get_info(device)
+    return kv_budget(total, free, gpu_memory_utilization, reserved_bytes)
+
+
+def max_blocks_per_seq(max_model_len: int, block_size: int, num_blocks: int) -> int:
+    """Width of the runner's static block tables: ``max_model_len // block_size + 2``, clamped to
+    the blocks the pool has (engine/model_runner.py:117, 284-288)."""
+    return min(int(max_model_len) // int(block_size) + 2, int(num_blocks))
+
+
 def allocate_kv_cache(num_layers: int, num_blocks: int, block_size: int, num_kv_heads: int,
                       head_dim: int, device: torch.device | str = "cuda",
                       dtype: torch.dtype = torch.bfloat16, zero: bool = True) -> torch.Tensor:

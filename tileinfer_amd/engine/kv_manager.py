@@ -94,6 +94,7 @@ class PagedKVManager:
         for _, slot in self.swapped.pop(seq.seq_id, []):
             self.host_free.append(slot)
         seq.block_table[:] = [b for b in seq.block_table if b >= 0]
+        seq.table_changed()
         return self.block_manager.deallocate(seq)
 
     def swap_out(self, seq: Sequence, max_blocks: int | None = None) -> list[tuple[int, int]]:
@@ -106,7 +107,7 @@ class PagedKVManager:
         if seq.seq_id in self.swapped:
             raise ValueError(f"sequence {seq.seq_id} is already swapped out")
         bm = self.block_manager
-        todo = [i for i, b in enumerate(seq.block_table) if b >= 0 and bm.blocks[b].ref_count == 1]
+        todo = [i for i, b in enumerate(seq.block_table) if b >= 0 and bm.ref_counts[b] == 1]
         if max_blocks is not None:
             todo = todo[:max_blocks]
         if len(todo) > len(self.host_free):
@@ -119,6 +120,8 @@ class PagedKVManager:
             record.append((i, slot))
             bm.release(seq.block_table[i])
             seq.block_table[i] = -1
+        if record:
+            seq.table_changed()
         self.swapped[seq.seq_id] = record
         return pairs
 
@@ -140,6 +143,8 @@ class PagedKVManager:
             seq.block_table[i] = bid
             pairs.append((slot, bid))
             self.host_free.append(slot)
+        if record:
+            seq.table_changed()
         return pairs
 
     def common_prefix_tokens(self, seqs: list[Sequence]) -> int:
@@ -159,5 +164,5 @@ class PagedKVManager:
     def shares_blocks(self, seqs: list[Sequence]) -> bool:
         """Whether any block of these sequences is held by more than one sequence: the decode
         hint ``kv_reuse`` (shared pages are then worth keeping in cache)."""
-        blocks = self.block_manager.blocks
-        return any(b >= 0 and blocks[b].ref_count > 1 for s in seqs for b in s.block_table)
+        refs = self.block_manager.ref_counts
+        return any(b >= 0 and refs[b] > 1 for s in seqs for b in s.block_table)

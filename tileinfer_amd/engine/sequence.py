@@ -29,7 +29,7 @@ class Sequence:
 
     __slots__ = ("seq_id", "status", "token_ids", "last_token", "num_tokens", "num_prompt_tokens",
                  "num_cached_tokens", "num_scheduled_tokens", "is_prefill", "block_table",
-                 "sampling_params")
+                 "table_generation", "sampling_params")
 
     def __init__(self, token_ids: _Seq[int], sampling_params: Any = None):
         if len(token_ids) == 0:
@@ -44,6 +44,9 @@ class Sequence:
         self.num_scheduled_tokens = 0    # tokens computed in the current step
         self.is_prefill = True
         self.block_table: list[int] = []
+        # Bumped whenever block_table is replaced or changed other than by appending (free,
+        # re-admission, swap), so a device-side copy of the table knows to re-send it whole.
+        self.table_generation = 0
         self.sampling_params = sampling_params
 
     def __len__(self) -> int:
@@ -70,6 +73,10 @@ class Sequence:
         if not 0 <= i < self.num_blocks:
             raise IndexError(f"block {i} out of range [0, {self.num_blocks})")
         return self.token_ids[i * self.block_size:(i + 1) * self.block_size]
+
+    def table_changed(self) -> None:
+        """Announce that ``block_table`` was replaced or edited in place (not just appended to)."""
+        self.table_generation += 1
 
     def append_token(self, token_id: int) -> None:
         self.token_ids.append(token_id)

@@ -109,6 +109,9 @@ def qknorm_rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         raise ValueError(f"k {tuple(k.shape)} / v {tuple(v.shape)} do not match q {tuple(q.shape)}")
     hkv = k.shape[1]
     dev, dt = q.device, q.dtype
+    if q_out is not None and (q_out.shape != (t, hq, d) or q_out.dtype != dt
+                              or q_out.device != dev or not _rows_ok(q_out)):
+        raise ValueError("q_out must be a [T, H_q, D] tensor of q's dtype and device")
     code = _lib.dtype_code(dt)
     if dev.type != "cuda":
         raise ValueError("qknorm_rope_append runs on the GPU; q is on " + str(dev))
