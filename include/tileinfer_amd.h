@@ -342,6 +342,29 @@ int ti_gqa_decode_paged_prefixed(const void* q, int64_t q_stride_b, int64_t q_st
                                  const float* prefix_o, const float* prefix_ml,
                                  int32_t prefix_tokens, void* stream);
 
+/*
+ * ti_gqa_decode_paged without a workspace argument, for callers that cannot allocate device memory
+ * (code under graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference (its decode allocates its output and a padded block table on every
+ * call, kernels/gqa_decode_paged.py:421-437). Same arguments and results as ti_gqa_decode_paged;
+ * the split-K partials go to a static device array of ti_gqa_decode_scratch_bytes() bytes
+ * (32 MiB) that each GPU the library runs on holds until the process ends. Calls whose plan needs
+ * more (ti_gqa_decode_plan's workspace_bytes) return TI_EINVAL. Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (different streams, or host threads) race and must be
+ * serialised by the caller. Allocates and frees nothing; the array's device address is looked up
+ * once per device on the first call.
+ */
+int ti_gqa_decode_paged_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                const void* k_cache, const void* v_cache,
+                                const int32_t* block_table, int64_t block_table_stride,
+                                const int32_t* seqlen, void* out, int32_t batch,
+                                int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                int32_t page_size, int64_t num_blocks, int32_t max_blocks_per_seq,
+                                int32_t split_tokens, int32_t variant, int32_t dtype, void* stream);
+
+/* Size in bytes of the per-GPU static scratch of ti_gqa_decode_paged_noalloc. */
+int64_t ti_gqa_decode_scratch_bytes(void);
+
 /* Text of the last error reported on the calling thread ("" when none). */
 const char* ti_last_error(void);
 

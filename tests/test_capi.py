@@ -182,3 +182,24 @@ def test_prefill_workspace_sizes():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="no non-HIP fallback"):
         _lib.load(tmp_path / "absent.so")
+
+
+def test_noalloc_decode_rejects_plans_beyond_its_scratch():
+    """A call whose split-K plan needs more than the static scratch is refused with a clear
+    error before anything is looked up or launched (no device needed)."""
+    lib = _lib.load()
+    cap = lib.ti_gqa_decode_scratch_bytes()
+    assert cap == 32 << 20
+    # 128 query heads over 8 KV heads: 128 balanced workgroups x 2 slots x 128 heads x (256 + 2)
+    # fp32 = 33.8 MB > 32 MiB.
+    s, m, w = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    _lib.check(lib.ti_gqa_decode_plan(64, 128, 8, 256, 16, 2048, 0, ctypes.byref(s),
+                                      ctypes.byref(m), ctypes.byref(w)))
+    assert w.value == m.value * 2 * 128 * 258 * 4 > cap
+    rc = lib.ti_gqa_decode_paged_noalloc(None, 0, 0, None, None, None, 2048, None, None, 64, 128,
+                                         8, 256, 16, 131072, 2048, 0, 0, 0, None)
+    assert rc == _lib.TI_EINVAL
+    assert b"no-allocation" in lib.ti_last_error() and b"scratch" in lib.ti_last_error()
+    # An empty batch that fits is a no-op.
+    assert lib.ti_gqa_decode_paged_noalloc(None, 0, 0, None, None, None, 0, None, None, 0, 24,
+                                           4, 256, 16, 0, 0, 0, 0, 0, None) == _lib.TI_OK

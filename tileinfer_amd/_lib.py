@@ -25,7 +25,7 @@ TI_DECODE_AUTO = 0
 TI_DECODE_MFMA = 1
 TI_DECODE_SCALAR = 2
 TI_DECODE_REUSE_KV = 0x10
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Every symbol declared in include/tileinfer_amd.h, with its ctypes signature.
 _c_i32, _c_i64, _c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
@@ -79,6 +79,11 @@ SIGNATURES = {
                                                  _c_vp, _c_vp, _c_vp, _c_i64, _c_i32, _c_i32,
                                                  _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32,
                                                  _c_i32, _c_i32, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "ti_gqa_decode_paged_noalloc": (ctypes.c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp,
+                                                   _c_i64, _c_vp, _c_vp, _c_i32, _c_i32, _c_i32,
+                                                   _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32,
+                                                   _c_i32, _c_vp]),
+    "ti_gqa_decode_scratch_bytes": (ctypes.c_int64, []),
     "ti_last_error": (ctypes.c_char_p, []),
     "ti_abi_version": (ctypes.c_int32, []),
 }

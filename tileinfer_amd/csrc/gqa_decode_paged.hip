@@ -26,6 +26,9 @@
 //     lane (n,g) holding head n at d in [128c+32g, +32).
 // Every O^T accumulator's head is its lane's head, so the softmax rescale needs no cross-lane
 // traffic; only the running max crosses the 4 lanes that share a head.
+#include <mutex>
+#include <vector>
+
 #include "decode_common.h"
 
 namespace ti {
@@ -769,6 +772,99 @@ extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_
                           block_table_stride, seqlen, out, workspace, workspace_bytes, batch,
                           num_q_heads, num_kv_heads, head_dim, page_size, num_blocks,
                           max_blocks_per_seq, split_tokens, variant, dtype, nullptr, 0, 0, stream);
+}
+
+// ---- No-allocation entry point -----------------------------------------------------------------
+//
+// For callers that cannot allocate (code under graph capture, tight serving loops): the split-K
+// partials live in a file-scope device array instead of a caller workspace. The array's host-side
+// name is not a device address; its address on each device comes from hipGetSymbolAddress, taken
+// once per device with that device current, and only that address is passed to kernels. Every call
+// on one device shares that device's array (calls that overlap on one GPU race on it). Nothing in
+// it needs to start at zero: the merge reads only partial slots the partial kernel of the same
+// call wrote.
+
+namespace ti {
+namespace {
+constexpr int64_t kDecodeScratchBytes = int64_t(32) << 20;  // 32 MiB per GPU, held for the process
+}  // namespace
+}  // namespace ti
+
+static __device__ __align__(256) unsigned char scratch[ti::kDecodeScratchBytes];
+
+namespace ti {
+namespace {
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // per device id: that device's address of `scratch`
+
+// The device address of `scratch` on the device `stream` belongs to (the current device for the
+// null stream), looked up on the first call for that device.
+int decode_scratch(hipStream_t stream, void** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return fail(TI_ELAUNCH, "no-alloc decode: hipGetDevice: %s", hipGetErrorString(e));
+  int dev = cur;
+  if (stream != nullptr) {
+    e = hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess) {
+      return fail(TI_ELAUNCH, "no-alloc decode: hipStreamGetDevice: %s", hipGetErrorString(e));
+    }
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (dev >= static_cast<int>(g_scratch_ptr.size())) g_scratch_ptr.resize(dev + 1, nullptr);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) {
+      return fail(TI_ELAUNCH, "no-alloc decode: hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+    }
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (e != hipSuccess || p == nullptr) {
+      return fail(TI_ELAUNCH, "no-alloc decode: hipGetSymbolAddress(scratch) on device %d: %s",
+                  dev, hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TI_OK;
+}
+
+}  // namespace
+}  // namespace ti
+
+extern "C" int64_t ti_gqa_decode_scratch_bytes(void) { return ti::kDecodeScratchBytes; }
+
+extern "C" int ti_gqa_decode_paged_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                           const void* k_cache, const void* v_cache,
+                                           const int32_t* block_table,
+                                           int64_t block_table_stride, const int32_t* seqlen,
+                                           void* out, int32_t batch, int32_t num_q_heads,
+                                           int32_t num_kv_heads, int32_t head_dim,
+                                           int32_t page_size, int64_t num_blocks,
+                                           int32_t max_blocks_per_seq, int32_t split_tokens,
+                                           int32_t variant, int32_t dtype, void* stream) {
+  using namespace ti;
+  Plan pl;
+  int rc = plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq,
+                split_tokens, &pl);
+  if (rc != TI_OK) return rc;
+  const bool balanced = (variant & 0xF) != TI_DECODE_SCALAR && pl.balanced_wgs > 0;
+  const int64_t need = balanced ? pl.ws_balanced : pl.ws_fixed;
+  if (need > kDecodeScratchBytes) {
+    return fail(TI_EINVAL,
+                "ti_gqa_decode_paged_noalloc: this call needs %lld bytes of split-K scratch, the "
+                "no-allocation entry point has %lld; use ti_gqa_decode_paged with a workspace",
+                (long long)need, (long long)kDecodeScratchBytes);
+  }
+  if (batch == 0) return TI_OK;
+  void* ws = nullptr;
+  rc = decode_scratch(static_cast<hipStream_t>(stream), &ws);
+  if (rc != TI_OK) return rc;
+  return decode_entry(q, q_stride_b, q_stride_h, k_cache, v_cache, block_table,
+                      block_table_stride, seqlen, out, ws, kDecodeScratchBytes, batch, num_q_heads,
+                      num_kv_heads, head_dim, page_size, num_blocks, max_blocks_per_seq,
+                      split_tokens, variant, dtype, nullptr, 0, 0, stream);
 }
 
 extern "C" int ti_gqa_decode_paged_gated(

@@ -26,7 +26,7 @@ import torch
 
 from .. import _lib
 
-__all__ = ["gqa_decode_paged_fn", "decode_plan"]
+__all__ = ["gqa_decode_paged_fn", "gqa_decode_paged_noalloc", "decode_plan"]
 
 _VARIANTS = {"auto": _lib.TI_DECODE_AUTO, "mfma": _lib.TI_DECODE_MFMA,
              "scalar": _lib.TI_DECODE_SCALAR}
@@ -61,6 +61,55 @@ def _static_i32(values: tuple, dev: torch.device) -> torch.Tensor:
 def _aligned_rows(t: torch.Tensor) -> bool:
     return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
             and all(s % 8 == 0 for s in t.stride()[:-1]))
+
+
+def _checked(q, k_cache, v_cache, block_table, seqlen_kv, page_size, variant):
+    """Validate a decode call's arguments; returns the (possibly made contiguous) q, table and
+    lengths with the sizes the library needs."""
+    if q.dim() != 3:
+        raise ValueError(f"q must be [B, H_q, D], got {tuple(q.shape)}")
+    b, h_q, d = q.shape
+    if k_cache.dim() != 4:
+        raise ValueError(f"k_cache must be [num_blocks, block_size, H_kv, D], got {tuple(k_cache.shape)}")
+    if v_cache.shape != k_cache.shape:
+        raise ValueError(f"v_cache shape {tuple(v_cache.shape)} != k_cache {tuple(k_cache.shape)}")
+    nb, bs, h_kv, d2 = k_cache.shape
+    if d2 != d:
+        raise ValueError(f"head_dim mismatch: q {d}, cache {d2}")
+    if h_kv <= 0 or h_q % h_kv != 0:
+        raise ValueError(f"H_q={h_q} is not a multiple of H_kv={h_kv}")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache and v_cache must be contiguous (a copy of the cache is never made)")
+    dt = q.dtype
+    if not (k_cache.dtype == v_cache.dtype == dt):
+        raise TypeError(f"dtype mismatch: q {dt}, k_cache {k_cache.dtype}, v_cache {v_cache.dtype}")
+    code = _lib.dtype_code(dt)
+    if block_table.dtype != torch.int32 or seqlen_kv.dtype != torch.int32:
+        raise TypeError(f"block_table/seqlen_kv must be int32, got {block_table.dtype}/{seqlen_kv.dtype}")
+    if block_table.dim() != 2 or block_table.shape[0] != b:
+        raise ValueError(f"block_table must be [{b}, W], got {tuple(block_table.shape)}")
+    if seqlen_kv.dim() != 1 or seqlen_kv.shape[0] != b:
+        raise ValueError(f"seqlen_kv must be [{b}], got {tuple(seqlen_kv.shape)}")
+    page_size = int(page_size)
+    rows = nb * bs
+    if page_size <= 0 or rows % page_size != 0:
+        raise ValueError(f"page_size {page_size} does not tile the cache's {rows} rows")
+    if variant not in _VARIANTS:
+        raise ValueError(f"variant must be one of {sorted(_VARIANTS)}, got {variant!r}")
+    dev = q.device
+    if dev.type != "cuda":
+        raise ValueError("gqa_decode_paged_fn runs on the GPU; q is on " + str(dev))
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache), ("block_table", block_table),
+                    ("seqlen_kv", seqlen_kv)):
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, q on {dev}")
+    if block_table.stride(-1) != 1:
+        block_table = block_table.contiguous()
+    if not seqlen_kv.is_contiguous():
+        seqlen_kv = seqlen_kv.contiguous()
+    if not _aligned_rows(q):
+        q = q.contiguous()
+    return q, block_table, seqlen_kv, (b, h_q, d, h_kv, rows, page_size, dt, code, dev)
 
 
 def gqa_decode_paged_fn(
@@ -108,49 +157,8 @@ def gqa_decode_paged_fn(
     Returns:
         [B, H_q, D] tensor in q's dtype.
     """
-    if q.dim() != 3:
-        raise ValueError(f"q must be [B, H_q, D], got {tuple(q.shape)}")
-    b, h_q, d = q.shape
-    if k_cache.dim() != 4:
-        raise ValueError(f"k_cache must be [num_blocks, block_size, H_kv, D], got {tuple(k_cache.shape)}")
-    if v_cache.shape != k_cache.shape:
-        raise ValueError(f"v_cache shape {tuple(v_cache.shape)} != k_cache {tuple(k_cache.shape)}")
-    nb, bs, h_kv, d2 = k_cache.shape
-    if d2 != d:
-        raise ValueError(f"head_dim mismatch: q {d}, cache {d2}")
-    if h_kv <= 0 or h_q % h_kv != 0:
-        raise ValueError(f"H_q={h_q} is not a multiple of H_kv={h_kv}")
-    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
-        raise ValueError("k_cache and v_cache must be contiguous (a copy of the cache is never made)")
-    dt = q.dtype
-    if not (k_cache.dtype == v_cache.dtype == dt):
-        raise TypeError(f"dtype mismatch: q {dt}, k_cache {k_cache.dtype}, v_cache {v_cache.dtype}")
-    code = _lib.dtype_code(dt)
-    if block_table.dtype != torch.int32 or seqlen_kv.dtype != torch.int32:
-        raise TypeError(f"block_table/seqlen_kv must be int32, got {block_table.dtype}/{seqlen_kv.dtype}")
-    if block_table.dim() != 2 or block_table.shape[0] != b:
-        raise ValueError(f"block_table must be [{b}, W], got {tuple(block_table.shape)}")
-    if seqlen_kv.dim() != 1 or seqlen_kv.shape[0] != b:
-        raise ValueError(f"seqlen_kv must be [{b}], got {tuple(seqlen_kv.shape)}")
-    page_size = int(page_size)
-    rows = nb * bs
-    if page_size <= 0 or rows % page_size != 0:
-        raise ValueError(f"page_size {page_size} does not tile the cache's {rows} rows")
-    if variant not in _VARIANTS:
-        raise ValueError(f"variant must be one of {sorted(_VARIANTS)}, got {variant!r}")
-    dev = q.device
-    if dev.type != "cuda":
-        raise ValueError("gqa_decode_paged_fn runs on the GPU; q is on " + str(dev))
-    for name, t in (("k_cache", k_cache), ("v_cache", v_cache), ("block_table", block_table),
-                    ("seqlen_kv", seqlen_kv)):
-        if t.device != dev:
-            raise ValueError(f"{name} is on {t.device}, q on {dev}")
-    if block_table.stride(-1) != 1:
-        block_table = block_table.contiguous()
-    if not seqlen_kv.is_contiguous():
-        seqlen_kv = seqlen_kv.contiguous()
-    if not _aligned_rows(q):
-        q = q.contiguous()
+    q, block_table, seqlen_kv, (b, h_q, d, h_kv, rows, page_size, dt, code, dev) = _checked(
+        q, k_cache, v_cache, block_table, seqlen_kv, page_size, variant)
     if out is None:
         out = torch.empty((b, h_q, d), dtype=dt, device=dev)
     elif (out.shape != (b, h_q, d) or out.dtype != dt or out.device != dev
@@ -207,4 +215,42 @@ def gqa_decode_paged_fn(
         return out
     _lib.check(lib.ti_gqa_decode_paged_gated(*args, g3.data_ptr(), g3.stride(0), g3.stride(1),
                                              _lib.stream_handle(dev)))
+    return out
+
+
+def gqa_decode_paged_noalloc(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seqlen_kv: torch.Tensor,
+    page_size: int = 16,
+    *,
+    out: torch.Tensor,
+    split_tokens: int | None = None,
+    variant: str = "auto",
+    kv_reuse: bool = False,
+) -> torch.Tensor:
+    """``gqa_decode_paged_fn`` for callers that cannot allocate: no output, workspace or copy is
+    made (``ti_gqa_decode_paged_noalloc``; the split-K partials live in the library's per-GPU
+    static scratch). ``out`` is required; ``q`` must have 16-byte aligned rows and the table and
+    lengths unit stride (they are refused rather than copied). Calls that overlap on one GPU share
+    that scratch and must not run concurrently. Results are bitwise those of
+    ``gqa_decode_paged_fn`` with the same plan."""
+    if not _aligned_rows(q) or block_table.stride(-1) != 1 or not seqlen_kv.is_contiguous():
+        raise ValueError("gqa_decode_paged_noalloc: q rows must be 16-byte aligned and the table "
+                         "and lengths unit-stride (no copies are made)")
+    _, _, _, (b, h_q, d, h_kv, rows, page_size, dt, code, dev) = _checked(
+        q, k_cache, v_cache, block_table, seqlen_kv, page_size, variant)
+    if (out.shape != (b, h_q, d) or out.dtype != dt or out.device != dev
+            or not out.is_contiguous()):
+        raise ValueError("out must be a contiguous [B, H_q, D] tensor of q's dtype and device")
+    width = block_table.shape[1]
+    lib = _lib.load()
+    _lib.check(lib.ti_gqa_decode_paged_noalloc(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+        block_table.data_ptr(), block_table.stride(0) if width > 0 else 0, seqlen_kv.data_ptr(),
+        out.data_ptr(), b, h_q, h_kv, d, page_size, rows // page_size, width,
+        int(split_tokens or 0), _VARIANTS[variant] | (_lib.TI_DECODE_REUSE_KV if kv_reuse else 0),
+        code, _lib.stream_handle(dev)))
     return out
