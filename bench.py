@@ -154,26 +154,61 @@ def parity_sample(kv, tables, seqlen, q, k_new, v_new, out_last, layer: int, idx
 
 def calibrate(dev, gib: float = 4.0, reps: int = 5):
     """Plain device copy and read of known size: the scale for rocprofv3 FETCH_SIZE/WRITE_SIZE
-    (bytes the counters report per byte moved) and the streaming bandwidth torch reaches."""
+    (bytes the counters report per byte moved) and the streaming bandwidth torch reaches. Then the
+    read ceiling of the decode's own pattern: ti_hbm_read_probe over one config-3 layer (131,072
+    pages of 32 KiB in K and in V, 8 GiB each) in pool order and through a random permutation cut
+    into 256 runs (the decode's balanced assignment), with the `nt` and the default load policy,
+    and the decode itself on the same memory in the same process."""
+    from tileinfer_amd import _lib
+
     n = int(gib * 2**30) // 2
     src = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
     dst = torch.empty_like(src)
     res = {}
     for name, fn, nbytes in (("copy", lambda: dst.copy_(src), 4 * n),
                              ("read_sum", lambda: src.sum(dtype=torch.float32), 2 * n)):
-        fn()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / reps
-        res[name] = {"bytes_per_launch": nbytes, "us": round(ms * 1e3, 1),
-                     "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        us = _time(fn, reps, 1)
+        res[name] = {"bytes_per_launch": nbytes, "us": round(us, 1),
+                     "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    del src, dst
     print(json.dumps({"calibration": res, "copy_read_bytes": 2 * n, "copy_write_bytes": 2 * n}),
           flush=True)
+
+    b, ctx = 64, 32768
+    nb = b * ctx // BLOCK
+    page_bytes = BLOCK * HKV * HEAD_DIM * 2
+    kv = torch.empty((2, nb, BLOCK, HKV, HEAD_DIM), dtype=torch.bfloat16, device=dev)
+    kv.normal_(generator=torch.Generator(device=dev).manual_seed(3))
+    perm = torch.randperm(nb, generator=torch.Generator(device=dev).manual_seed(4),
+                          device=dev).to(torch.int32)
+    sink = torch.empty(2048 * 256 * 4, dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    stream = _lib.stream_handle(dev)
+    read_bytes = 2 * nb * page_bytes
+    ceiling = {}
+    for pattern, pages, runs, wgs in (("pool_order_runs256", None, 1, 256),
+                                      ("permuted_runs256", perm, 1, 256),
+                                      ("permuted_gridstride2048", perm, 0, 2048)):
+        for policy, streaming in (("nt", 1), ("default", 0)):
+            def probe():
+                _lib.check(lib.ti_hbm_read_probe(
+                    kv[0].data_ptr(), kv[1].data_ptr(),
+                    pages.data_ptr() if pages is not None else None, nb, page_bytes, nb,
+                    streaming, runs, wgs, sink.data_ptr(), stream))
+            us = _time(probe, reps, 1)
+            ceiling[f"{pattern}_{policy}"] = {"us": round(us, 1),
+                                              "GBps": round(read_bytes / (us * 1e-6) / 1e9, 1)}
+    q = torch.randn((b, HQ, HEAD_DIM), generator=torch.Generator(device=dev).manual_seed(5),
+                    device=dev).to(torch.bfloat16)
+    seqlen = torch.full((b,), ctx, dtype=torch.int32, device=dev)
+    table = perm.view(b, ctx // BLOCK)
+    us = _time(lambda: gqa_decode_paged_fn(q, kv[0], kv[1], table, seqlen, BLOCK), reps, 1)
+    d_bytes = decode_bytes([ctx] * b)
+    dec = {"us": round(us, 1), "GBps": round(d_bytes / (us * 1e-6) / 1e9, 1)}
+    dec["fraction_of_permuted_runs256_nt"] = round(
+        dec["GBps"] / ceiling["permuted_runs256_nt"]["GBps"], 4)
+    print(json.dumps({"read_ceiling": ceiling, "read_bytes_per_launch": read_bytes,
+                      "decode_same_memory": dec}), flush=True)
 
 
 def _time(fn, steps: int, warmup: int) -> float:
@@ -404,6 +439,57 @@ def prefill_config4(st, chunk_slots, kc, vc, dev, args) -> dict:
             "peak_TFLOPs_bf16_dense": 2500.0}
 
 
+def metric_extras(kv, tables, seqlen, q, dev, args) -> dict:
+    """The rest of the metric on the same cache (layer 0's pool, after the timed steps):
+    * append GB/s at config 4's N = 2,080 (a 2,048-token chunk over 128 random blocks + 32 decode
+      tokens) and at a bulk N = 65,536 (random distinct slots), as the reference benches a bulk
+      store (kernels/kvcache_store.py:117-123);
+    * the decode at the configured 2,048-token partitions (config 3) beside the balanced default;
+    * a batch-64 decode sweep over context 1k..32k (each sequence's first ctx/16 blocks of its
+      permuted table), % of peak per point, as the reference's seqlen sweep
+      (kernels/gqa_decode_paged.py:614-656).
+    All timed with HIP events on the launch stream (mean over --steps calls after --warmup)."""
+    k_rows, v_rows, k_paged, v_paged = layer_views(kv, 0)
+    nb = k_paged.shape[0]
+    b, full_ctx = seqlen.shape[0], int(seqlen[0])
+    gen = torch.Generator(device=dev).manual_seed(7)
+    rnd = lambda *sh: torch.randn(sh, generator=gen, device=dev).to(torch.bfloat16)  # noqa: E731
+    gbps = lambda nbytes, us: round(nbytes / (us * 1e-6) / 1e9, 1)  # noqa: E731
+    res = {}
+    blocks = torch.randperm(nb, generator=gen, device=dev)[:160].long()
+    chunk = (blocks[:128, None] * BLOCK + torch.arange(BLOCK, device=dev)).reshape(-1)
+    dec = blocks[128:] * BLOCK + torch.randint(0, BLOCK, (32,), generator=gen, device=dev)
+    for name, slots in (("append_2080", torch.cat([chunk, dec]).to(torch.int32)),
+                        ("append_65536", torch.randperm(nb * BLOCK, generator=gen,
+                                                        device=dev)[:65536].to(torch.int32))):
+        n = slots.numel()
+        key, val = rnd(n, HKV, HEAD_DIM), rnd(n, HKV, HEAD_DIM)
+        us = _time(lambda: store_kvcache(key, val, k_rows, v_rows, slots), args.steps, args.warmup)
+        nbytes = append_bytes(slots, HKV * HEAD_DIM)
+        res[name] = {"tokens": n, "us": round(us, 2), "GBps_algorithmic": gbps(nbytes, us),
+                     "pct_of_peak_hbm": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 1)}
+    d_bytes = decode_bytes([full_ctx] * b)
+    for name, split in (("decode_balanced", None), ("decode_split_2048", 2048)):
+        us = _time(lambda: gqa_decode_paged_fn(q[0], k_paged, v_paged, tables[0], seqlen, BLOCK,
+                                               split_tokens=split), args.steps, args.warmup)
+        res[name] = {"ctx": full_ctx, "us": round(us, 2), "GBps_algorithmic": gbps(d_bytes, us),
+                     "pct_of_peak_hbm": round(100 * d_bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 2)}
+    sweep = []
+    ctx = 1024
+    while ctx <= full_ctx:
+        tb = tables[0][:, :ctx // BLOCK]
+        sl = torch.full((b,), ctx, dtype=torch.int32, device=dev)
+        us = _time(lambda: gqa_decode_paged_fn(q[0], k_paged, v_paged, tb, sl, BLOCK),
+                   args.steps, args.warmup)
+        nbytes = decode_bytes([ctx] * b)
+        sweep.append({"ctx": ctx, "us": round(us, 2), "GBps_algorithmic": gbps(nbytes, us),
+                      "pct_of_peak_hbm": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+                                               2)})
+        ctx *= 2
+    res["decode_ctx_sweep_batch64"] = sweep
+    return res
+
+
 def config_parity(cfg: int, st, key, val, slots, out, dev) -> dict:
     """Parity on the run itself: appended rows bit-exact; the decode output of every sequence
     against the CPU oracle (max abs error; max relative error over outputs with |ref| >= 0.05;
@@ -587,6 +673,8 @@ def main():
                     help="skip the unfused-vs-fused timing of the element-wise work around attention")
     ap.add_argument("--no-metadata", action="store_true",
                     help="skip the per-step metadata comparison (host builder vs device tables)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the append sizes, 2,048-token partitions and context sweep")
     ap.add_argument("--sequential-tables", action="store_true",
                     help="diagnostic: contiguous blocks per sequence instead of random permutations")
     args = ap.parse_args()
@@ -710,6 +798,9 @@ def main():
     if not args.no_parity:
         log("full-size parity sample")
         result["parity"] = parity_sample(kv, tables, seqlen, q, k_new, v_new, out, layers - 1)
+    if not args.no_extras:
+        log("append at N=2,080 / 65,536, decode at 2,048-token partitions, context sweep")
+        result["extras"] = metric_extras(kv, tables, seqlen, q, dev, args)
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle) on a sample")
         result["cpu_baseline"] = cpu_baseline(kv, tables, seqlen, q, k_new, v_new)
