@@ -443,7 +443,8 @@ def metric_extras(kv, tables, seqlen, q, dev, args) -> dict:
     """The rest of the metric on the same cache (layer 0's pool, after the timed steps):
     * append GB/s at config 4's N = 2,080 (a 2,048-token chunk over 128 random blocks + 32 decode
       tokens) and at a bulk N = 65,536 (random distinct slots), as the reference benches a bulk
-      store (kernels/kvcache_store.py:117-123);
+      store (kernels/kvcache_store.py:117-123); GPU time from a captured graph, since back-to-back
+      eager calls of a few-µs kernel measure the Python wrapper;
     * the decode at the configured 2,048-token partitions (config 3) beside the balanced default;
     * a batch-64 decode sweep over context 1k..32k (each sequence's first ctx/16 blocks of its
       permuted table), % of peak per point, as the reference's seqlen sweep
@@ -464,10 +465,15 @@ def metric_extras(kv, tables, seqlen, q, dev, args) -> dict:
                                                         device=dev)[:65536].to(torch.int32))):
         n = slots.numel()
         key, val = rnd(n, HKV, HEAD_DIM), rnd(n, HKV, HEAD_DIM)
-        us = _time(lambda: store_kvcache(key, val, k_rows, v_rows, slots), args.steps, args.warmup)
+        fn = lambda: store_kvcache(key, val, k_rows, v_rows, slots)  # noqa: E731
+        eager = _time(fn, args.steps, args.warmup)
+        us = _graph_us(fn)
         nbytes = append_bytes(slots, HKV * HEAD_DIM)
         res[name] = {"tokens": n, "us": round(us, 2), "GBps_algorithmic": gbps(nbytes, us),
-                     "pct_of_peak_hbm": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 1)}
+                     "pct_of_peak_hbm": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 1),
+                     "us_eager_call": round(eager, 2),
+                     "timing": "us: GPU time per call from a captured graph of 20 calls; "
+                               "us_eager_call: back-to-back Python calls (host-bound when small)"}
     d_bytes = decode_bytes([full_ctx] * b)
     for name, split in (("decode_balanced", None), ("decode_split_2048", 2048)):
         us = _time(lambda: gqa_decode_paged_fn(q[0], k_paged, v_paged, tables[0], seqlen, BLOCK,

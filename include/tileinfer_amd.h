@@ -199,11 +199,14 @@ int ti_gqa_prefill_paged_gated(const void* q, int64_t q_stride_t, int64_t q_stri
 
 /*
  * ti_gqa_prefill_paged with unnormalised fp32 output, for merging with attention over other keys:
- *   o_part  [total_q, num_q_heads, head_dim] fp32, o relative to 2^m (16-byte aligned)
- *   ml_part [total_q, num_q_heads, 2] fp32 (m, l): m the running maximum of the scaled scores in
- *           exp2 units (-inf: no visible key), l the sum of 2^(s - m)
- * so that out = o_part / l. No reference counterpart: it is the prefix half of
- * ti_gqa_decode_paged_prefixed (a shared prefix attended once for a whole decode batch).
+ *   o_part  [key_splits, total_q, num_q_heads, head_dim] fp32, o relative to 2^m (16-byte aligned)
+ *   ml_part [key_splits, total_q, num_q_heads, 2] fp32 (m, l): m the running maximum of the scaled
+ *           scores in exp2 units (-inf: no visible key), l the sum of 2^(s - m)
+ * so that out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s, M = max_s m_s. key_splits = 1 is
+ * one part per row (any schedule); key_splits > 1 cuts every unit's keys into that many contiguous
+ * ranges, one workgroup and one part each (per-unit schedule: workspace must be NULL). No reference
+ * counterpart: it is the prefix half of ti_gqa_decode_paged_prefixed (a shared prefix attended once
+ * for a whole decode batch).
  */
 int ti_gqa_prefill_paged_partial(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                                  const void* k_cache, const void* v_cache,
@@ -214,7 +217,15 @@ int ti_gqa_prefill_paged_partial(const void* q, int64_t q_stride_t, int64_t q_st
                                  int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
                                  int32_t head_dim, int32_t page_size, int64_t num_blocks,
                                  int32_t max_blocks_per_seq, int32_t causal, int32_t dtype,
-                                 void* stream);
+                                 int32_t key_splits, void* stream);
+
+/*
+ * Key splits for a one-sequence ti_gqa_prefill_paged_partial pass of total_q queries over
+ * kv_tokens keys (the shared prefix of a decode batch): enough workgroups to give every compute
+ * unit one, each key range at least 4 key tiles; 1 when splitting does not pay. Host-only.
+ */
+int32_t ti_gqa_prefill_key_splits(int32_t total_q, int32_t num_q_heads, int32_t num_kv_heads,
+                                  int32_t head_dim, int32_t kv_tokens);
 
 /*
  * Workspace of the balanced ti_gqa_prefill_paged schedule for these sizes (host-only, no device
@@ -322,8 +333,10 @@ int ti_gqa_decode_paged_gated(const void* q, int64_t q_stride_b, int64_t q_strid
  * ti_gqa_decode_paged (optionally gated) for a batch whose sequences share their first
  * prefix_tokens tokens (a multiple of page_size): the kernel attends to tokens
  * [prefix_tokens, seqlen[b]) of each sequence, through block_table columns from
- * prefix_tokens / page_size on, and merges into every row the precomputed prefix part
- * (prefix_o [B, H_q, D], prefix_ml [B, H_q, 2], as ti_gqa_prefill_paged_partial writes them).
+ * prefix_tokens / page_size on, and merges into every row the precomputed prefix parts
+ * (prefix_o [prefix_parts, B, H_q, D], prefix_ml [prefix_parts, B, H_q, 2], as
+ * ti_gqa_prefill_paged_partial writes them with key_splits = prefix_parts), in part order. Rows
+ * with seqlen[b] < prefix_tokens (graph padding) get no prefix part.
  * Same arguments as ti_gqa_decode_paged_gated otherwise (gate may be NULL); the workspace is
  * ti_gqa_decode_plan's for max_blocks_per_seq - prefix_tokens / page_size. MFMA variant only.
  * Reference counterpart: gqa_decode_paged_fn (kernels/gqa_decode_paged.py:392-437) on a batch
@@ -340,7 +353,7 @@ int ti_gqa_decode_paged_prefixed(const void* q, int64_t q_stride_b, int64_t q_st
                                  int32_t split_tokens, int32_t variant, int32_t dtype,
                                  const void* gate, int64_t gate_stride_b, int64_t gate_stride_h,
                                  const float* prefix_o, const float* prefix_ml,
-                                 int32_t prefix_tokens, void* stream);
+                                 int32_t prefix_parts, int32_t prefix_tokens, void* stream);
 
 /*
  * ti_gqa_decode_paged without a workspace argument, for callers that cannot allocate device memory

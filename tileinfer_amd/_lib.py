@@ -25,7 +25,7 @@ TI_DECODE_AUTO = 0
 TI_DECODE_MFMA = 1
 TI_DECODE_SCALAR = 2
 TI_DECODE_REUSE_KV = 0x10
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # Every symbol declared in include/tileinfer_amd.h, with its ctypes signature.
 _c_i32, _c_i64, _c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
@@ -54,13 +54,14 @@ SIGNATURES = {
                                                     _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                                     _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
                                                     _c_i32, _c_i32, _c_i32, _c_i64, _c_i32,
-                                                    _c_i32, _c_i32, _c_vp]),
+                                                    _c_i32, _c_i32, _c_i32, _c_vp]),
+    "ti_gqa_prefill_key_splits": (ctypes.c_int32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "ti_gqa_decode_paged_prefixed": (ctypes.c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp,
                                                     _c_i64, _c_vp, _c_vp, _c_vp, _c_i64, _c_i32,
                                                     _c_i32, _c_i32, _c_i32, _c_i32, _c_i64,
                                                     _c_i32, _c_i32, _c_i32, _c_i32, _c_vp,
                                                     _c_i64, _c_i64, _c_vp, _c_vp, _c_i32,
-                                                    _c_vp]),
+                                                    _c_i32, _c_vp]),
     "ti_gqa_prefill_workspace_bytes": (ctypes.c_int, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                                       _c_i32, _c_i32, _I64P]),
     "ti_paged_metadata": (ctypes.c_int, [_c_vp, _c_i64, _c_i32, _c_i32, _c_vp, _c_vp, _c_vp,

@@ -122,12 +122,14 @@ struct DecodeArgs {
   // strides; nullptr for the plain output.
   const uint16_t* gate;
   int64_t gate_sb, gate_sh;
-  // Optional attention part computed elsewhere (a prefix shared by the batch): unnormalised fp32
-  // o relative to 2^m [B, hq, D] and (m, l) [B, hq, 2], m in exp2 units, merged into every row;
-  // the kernel itself then covers tokens [ctx_offset, seqlen[b]) through the block table it gets
-  // (whose column 0 is token ctx_offset's page). nullptr / 0 for plain decode.
+  // Optional attention parts computed elsewhere (a prefix shared by the batch): pre_parts
+  // unnormalised fp32 parts, o relative to 2^m [pre_parts][B][hq][D] and (m, l)
+  // [pre_parts][B][hq][2], m in exp2 units, merged into every row in part order; the kernel itself
+  // then covers tokens [ctx_offset, seqlen[b]) through the block table it gets (whose column 0 is
+  // token ctx_offset's page). nullptr / 0 for plain decode.
   const float* pre_o;
   const float* pre_ml;
+  int32_t pre_parts;
   int32_t ctx_offset;
 };
 

@@ -220,51 +220,71 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
   };
 
   auto store_out = [&](int b) {
-    // With a precomputed part (m_e, l_e, o_e): out = (w o + w_e o_e) / (w l + w_e l_e), weights
-    // 2^(m - M) and 2^(m_e - M), M the larger maximum.
-    float ws = 1.f, we = 0.f, l = l_tot;
-    const float* erow = nullptr;
-    // A row shorter than the shared prefix (the runner's graph-padding rows: context 1, no
-    // pages) is outside the prefix contract and gets no prefix part: zeros, as plain decode.
-    if (a.pre_o && a.seqlen[b] >= a.ctx_offset) {  // uniform
-      const int64_t r = int64_t(b) * a.hq + h;
-      const float me = a.pre_ml[2 * r], le = a.pre_ml[2 * r + 1];
-      const float mm = fmaxf(m_run, me);
-      ws = m_run == -INFINITY ? 0.f : fast_exp2(m_run - mm);
-      we = me == -INFINITY ? 0.f : fast_exp2(me - mm);
-      l = ws * l_tot + we * le;
-      erow = a.pre_o + r * D;
-    }
-    const float inv = l > 0.f ? 1.f / l : 0.f;
     uint16_t* orow = a.out + (int64_t(b) * a.hq + h) * D;
     const uint16_t* grow = a.gate ? a.gate + b * a.gate_sb + int64_t(h) * a.gate_sh : nullptr;
+    auto put = [&](int d, u32x4 w) __attribute__((always_inline)) {
+      if (grow) {
+        const u32x4 gv = load16(grow + d);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = gate_mul2(w[k], gv[k], Tag{});
+      }
+      *reinterpret_cast<u32x4*>(orow + d) = w;
+    };
+    // A row shorter than the shared prefix (the runner's graph-padding rows: context 1, no
+    // pages) is outside the prefix contract and gets no prefix part: zeros, as plain decode.
+    if (!a.pre_o || a.seqlen[b] < a.ctx_offset) {  // uniform
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          u32x4 w;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            w[k] = pack2(o[8 * c + 2 * k][r] * inv, o[8 * c + 2 * k + 1][r] * inv, Tag{});
+          }
+          put(128 * c + 32 * g + 8 * r, w);
+        }
+      }
+      return;
+    }
+    // With the prefix parts (m_s, l_s, o_s): out = (w o + sum_s w_s o_s) / (w l + sum_s w_s l_s),
+    // weights 2^(m - M) and 2^(m_s - M), M the largest maximum; parts in order.
+    const int64_t r0 = int64_t(b) * a.hq + h;
+    const int64_t part_rows = int64_t(batch) * a.hq;
+    float mm = m_run;
+    for (int s = 0; s < a.pre_parts; ++s) mm = fmaxf(mm, a.pre_ml[2 * (s * part_rows + r0)]);
+    const float ws = m_run == -INFINITY ? 0.f : fast_exp2(m_run - mm);
+    float l = ws * l_tot;
+    for (int s = 0; s < a.pre_parts; ++s) {
+      const float me = a.pre_ml[2 * (s * part_rows + r0)];
+      l += (me == -INFINITY ? 0.f : fast_exp2(me - mm)) * a.pre_ml[2 * (s * part_rows + r0) + 1];
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int d = 128 * c + 32 * g + 8 * r;
+        float acc[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] = o[8 * c + k][r] * ws;
+        for (int s = 0; s < a.pre_parts; ++s) {
+          const int64_t pr = s * part_rows + r0;
+          const float me = a.pre_ml[2 * pr];
+          const float we = me == -INFINITY ? 0.f : fast_exp2(me - mm);
+          const f32x4 e0 = *reinterpret_cast<const f32x4*>(a.pre_o + pr * D + d);
+          const f32x4 e1 = *reinterpret_cast<const f32x4*>(a.pre_o + pr * D + d + 4);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            acc[k] += e0[k] * we;
+            acc[4 + k] += e1[k] * we;
+          }
+        }
         u32x4 w;
-        if (erow) {
-          const f32x4 e0 = *reinterpret_cast<const f32x4*>(erow + d);
-          const f32x4 e1 = *reinterpret_cast<const f32x4*>(erow + d + 4);
-          const float ev[8] = {e0[0], e0[1], e0[2], e0[3], e1[0], e1[1], e1[2], e1[3]};
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            w[k] = pack2((o[8 * c + 2 * k][r] * ws + ev[2 * k] * we) * inv,
-                         (o[8 * c + 2 * k + 1][r] * ws + ev[2 * k + 1] * we) * inv, Tag{});
-          }
-        } else {
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            w[k] = pack2(o[8 * c + 2 * k][r] * inv, o[8 * c + 2 * k + 1][r] * inv, Tag{});
-          }
-        }
-        if (grow) {
-          const u32x4 gv = load16(grow + d);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) w[k] = gate_mul2(w[k], gv[k], Tag{});
-        }
-        *reinterpret_cast<u32x4*>(orow + d) = w;
+        for (int k = 0; k < 4; ++k) w[k] = pack2(acc[2 * k] * inv, acc[2 * k + 1] * inv, Tag{});
+        put(d, w);
       }
     }
   };
@@ -382,6 +402,28 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
     if (grow) w = gate_mul2(w, *reinterpret_cast<const uint32_t*>(grow + j), Tag{});
     *reinterpret_cast<uint32_t*>(orow + j) = w;
   };
+  // The precomputed prefix parts of this row (none for rows shorter than the prefix, see the
+  // partial kernel's store_out): their largest maximum, and their weighted sum at a given maximum.
+  const int64_t pr = int64_t(b) * a.hq + h;
+  const int64_t part_rows = int64_t(batch) * a.hq;
+  const bool pre = a.pre_o != nullptr && a.seqlen[b] >= a.ctx_offset;
+  float me = -INFINITY;
+  if (pre) {
+    for (int s = 0; s < a.pre_parts; ++s) me = fmaxf(me, a.pre_ml[2 * (s * part_rows + pr)]);
+  }
+  // acc += sum_s 2^(m_s - m) o_s, returns sum_s 2^(m_s - m) l_s (parts in order).
+  auto add_pre = [&](float m, float* acc) -> float {
+    float l = 0.f;
+    for (int s = 0; s < a.pre_parts; ++s) {
+      const int64_t r = s * part_rows + pr;
+      const float ms = a.pre_ml[2 * r];
+      const float w = ms == -INFINITY ? 0.f : fast_exp2(ms - m);
+#pragma unroll
+      for (int q = 0; q < PER; ++q) acc[q] += w * a.pre_o[r * D + d0 + q];
+      l += w * a.pre_ml[2 * r + 1];
+    }
+    return l;
+  };
   int64_t slot0 = 0, stride = 1;
   int nparts = 0;
   int first_part_slot1 = 0;  // balanced: the first part sits in slot 1 of its workgroup
@@ -392,38 +434,34 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
     slot0 = (int64_t(b) * a.hq + h) * a.max_splits;
   } else {
     const int nb = seq_tiles(a, b);
-    if (nb == 0) {  // no token of this kernel's range: zeros, or the precomputed part alone
+    if (nb == 0) {  // no token of this kernel's range: zeros, or the prefix parts alone
       float e[PER];
+#pragma unroll
+      for (int q = 0; q < PER; ++q) e[q] = 0.f;
       float inv = 0.f;
-      if (a.pre_o && a.seqlen[b] >= a.ctx_offset) {  // shorter rows: zeros (see store_out)
-        const int64_t r = int64_t(b) * a.hq + h;
-        const float le = a.pre_ml[2 * r + 1];
-        inv = (a.pre_ml[2 * r] != -INFINITY && le > 0.f) ? 1.f / le : 0.f;
-#pragma unroll
-        for (int q = 0; q < PER; ++q) e[q] = a.pre_o[r * D + d0 + q];
-      } else {
-#pragma unroll
-        for (int q = 0; q < PER; ++q) e[q] = 0.f;
+      if (me != -INFINITY) {
+        const float l = add_pre(me, e);
+        inv = l > 0.f ? 1.f / l : 0.f;
       }
 #pragma unroll
       for (int j = 0; j < PER; j += 2) put(j, pack2(e[j] * inv, e[j + 1] * inv, Tag{}));
       return;
     }
-    int tot = 0, pre = 0;
+    int tot = 0, pre_tiles = 0;
     for (int b0 = 0; b0 < batch; b0 += 64) {
       const int j = b0 + lane;
       const int nt = j < batch ? seq_tiles(a, j) : 0;
       tot += nt;
-      pre += j < b ? nt : 0;
+      pre_tiles += j < b ? nt : 0;
     }
     tot = wave_sum(tot);
-    pre = wave_sum(pre);
+    pre_tiles = wave_sum(pre_tiles);
     const int chunk = balanced_chunk(a, tot);
-    const int i0 = pre / chunk;
-    const int i1 = (pre + nb - 1) / chunk;
+    const int i0 = pre_tiles / chunk;
+    const int i1 = (pre_tiles + nb - 1) / chunk;
     if (i0 == i1) return;  // one workgroup covered the whole sequence and wrote it
     nparts = i1 - i0 + 1;
-    first_part_slot1 = (i0 * chunk < pre) ? 1 : 0;
+    first_part_slot1 = (i0 * chunk < pre_tiles) ? 1 : 0;
     slot0 = int64_t(i0) * 2 * a.hq + h;
     stride = 2 * a.hq;
   }
@@ -431,7 +469,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
   auto part = [&](int s) -> int64_t {
     return slot0 + s * stride + ((s == 0 && first_part_slot1) ? a.hq : 0);
   };
-  // Maximum over the parts' m (and the precomputed part's), lane-parallel.
+  // Maximum over the parts' m (and the prefix parts'), lane-parallel.
   float m = -INFINITY;
   for (int s0 = 0; s0 < nparts; s0 += 64) {
     const int s = s0 + lane;
@@ -439,19 +477,12 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
   }
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
-  const int64_t pr = int64_t(b) * a.hq + h;
-  const float me = a.pre_o ? a.pre_ml[2 * pr] : -INFINITY;
   m = fmaxf(m, me);
   float acc[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) acc[j] = 0.f;
   float l = 0.f;
-  if (me != -INFINITY) {  // the precomputed part first (fixed order)
-    const float we = fast_exp2(me - m);
-#pragma unroll
-    for (int q = 0; q < PER; ++q) acc[q] = we * a.pre_o[pr * D + d0 + q];
-    l = we * a.pre_ml[2 * pr + 1];
-  }
+  if (me != -INFINITY) l = add_pre(m, acc);  // the prefix parts first (fixed order)
   if (m != -INFINITY) {
     // Parts in chunks of 64: lane s holds part s0+s's weight; the o rows of 8 parts are loaded
     // back to back so their latencies overlap. Summation order is fixed (ascending part).
@@ -651,7 +682,7 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
                  int32_t split_tokens, int32_t variant, int32_t dtype, const void* gate,
                  int64_t gate_stride_b, int64_t gate_stride_h, void* stream,
                  const float* pre_o = nullptr, const float* pre_ml = nullptr,
-                 int32_t prefix_tokens = 0) {
+                 int32_t prefix_tokens = 0, int32_t prefix_parts = 0) {
   if (dtype != TI_DTYPE_BF16 && dtype != TI_DTYPE_F16) {
     return fail(TI_EUNSUPPORTED, "ti_gqa_decode_paged: dtype code %d is not bf16/fp16", dtype);
   }
@@ -727,6 +758,7 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
   a.gate_sh = gate_stride_h;
   a.pre_o = pre_o;
   a.pre_ml = pre_ml;
+  a.pre_parts = pre_o ? prefix_parts : 0;
   a.ctx_offset = prefix_tokens;
   if (pre_o != nullptr && kind == TI_DECODE_SCALAR) {
     return fail(TI_EUNSUPPORTED, "ti_gqa_decode_paged_prefixed: MFMA variant only");
@@ -892,10 +924,15 @@ extern "C" int ti_gqa_decode_paged_prefixed(
     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
     int64_t num_blocks, int32_t max_blocks_per_seq, int32_t split_tokens, int32_t variant,
     int32_t dtype, const void* gate, int64_t gate_stride_b, int64_t gate_stride_h,
-    const float* prefix_o, const float* prefix_ml, int32_t prefix_tokens, void* stream) {
+    const float* prefix_o, const float* prefix_ml, int32_t prefix_parts, int32_t prefix_tokens,
+    void* stream) {
   using namespace ti;
   if (batch > 0 && (prefix_o == nullptr || prefix_ml == nullptr)) {
     return fail(TI_EINVAL, "ti_gqa_decode_paged_prefixed: null prefix part");
+  }
+  if (prefix_parts < 1 || prefix_parts > 65535) {
+    return fail(TI_EINVAL, "ti_gqa_decode_paged_prefixed: prefix_parts %d outside [1, 65535]",
+                prefix_parts);
   }
   if (prefix_tokens < 0 || page_size <= 0 || prefix_tokens % page_size != 0 ||
       prefix_tokens / page_size > max_blocks_per_seq) {
@@ -912,5 +949,5 @@ extern "C" int ti_gqa_decode_paged_prefixed(
                       workspace, workspace_bytes, batch, num_q_heads, num_kv_heads, head_dim,
                       page_size, num_blocks, max_blocks_per_seq - skip, split_tokens, variant,
                       dtype, gate, gate_stride_b, gate_stride_h, stream, prefix_o, prefix_ml,
-                      prefix_tokens);
+                      prefix_tokens, prefix_parts);
 }

@@ -56,10 +56,14 @@ struct PrefillArgs {
   // these strides; nullptr for the plain output.
   const uint16_t* gate;
   int64_t gate_st, gate_sh;
-  // Unnormalised output (instead of out): fp32 o relative to 2^m, [total_q][hq][D], and (m, l)
-  // [total_q][hq][2], m in exp2 units; nullptr for the normalised output.
+  // Unnormalised output (instead of out): fp32 o relative to 2^m, [key_splits][total_q][hq][D],
+  // and (m, l) [key_splits][total_q][hq][2], m in exp2 units; nullptr for the normalised output.
   float* uo;
   float* uml;
+  // Per-unit schedule only: each unit's key tiles are cut into key_splits contiguous ranges, one
+  // workgroup each (grid z = sequence * key_splits + split), and split s writes its unnormalised
+  // part to slot s of uo / uml (a range with no key writes m = -inf, l = 0, o = 0). 1 otherwise.
+  int32_t key_splits;
 };
 
 constexpr float kRescaleSlack = 8.f;  // exp2 units a row maximum may rise before O is rescaled
@@ -364,8 +368,8 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   // The sub-tile this wave loads (kKT / W rows per wave, inside one sub-tile).
   const int my_sub = (min(wave, LW - 1) * (kKT / LW)) / 16;
 
-  // The current unit (uniform) and this lane's C rows of it.
-  int b = 0, kvh = 0, qb0 = 0;
+  // The current unit (uniform) and this lane's C rows of it; the key split of the unit.
+  int b = 0, kvh = 0, qb0 = 0, split = 0;
   SeqExtent sx;
   const int32_t* bt_row = a.block_table;
   int wave_last_key = 0, wave_first_key = 0;
@@ -691,8 +695,8 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       const int rho = wave * 16 * C + 16 * c + n;
       const int tok = rho / G;
       const int hh = rho - tok * G;
-      if (a.uo) {  // uniform: unnormalised rows for a later merge
-        const int64_t r = int64_t(sx.q_start + qb0 + tok) * a.hq + kvh * G + hh;
+      if (a.uo) {  // uniform: unnormalised rows for a later merge (slot of the key split)
+        const int64_t r = (int64_t(split) * a.total_q + sx.q_start + qb0 + tok) * a.hq + kvh * G + hh;
 #pragma unroll
         for (int dt = 0; dt < NT; ++dt) {
           *reinterpret_cast<f32x4*>(a.uo + r * D + 16 * dt + 4 * g) = o[c][dt];
@@ -755,14 +759,21 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   const PlanView v = plan_view(a);
   int p = 0, n_pairs = 1, grid_nt = 0, unit_work = 1;
   int64_t pos = 0, end = 0;  // this workgroup's work positions (balanced)
+  int grid_t0 = 0;  // per-unit schedule: the key tiles [grid_t0, grid_nt) of this workgroup
   if (!balanced) {
     // The heaviest query blocks (latest tokens, longest causal range) are dispatched first.
     kvh = blockIdx.x;
-    b = blockIdx.z;
+    b = blockIdx.z / a.key_splits;
+    split = blockIdx.z - b * a.key_splits;
     qb0 = (gridDim.y - 1 - blockIdx.y) * a.tq;
     const SeqExtent s0 = seq_extent(a, b);
     if (qb0 >= s0.q_len) return;  // uniform over the workgroup
     grid_nt = (block_key_end(a, s0, qb0) + kKT - 1) / kKT;
+    if (a.key_splits > 1) {
+      const int per = (grid_nt + a.key_splits - 1) / a.key_splits;
+      grid_t0 = min(split * per, grid_nt);
+      grid_nt = min(grid_t0 + per, grid_nt);
+    }
   } else {
     p = __builtin_amdgcn_readfirstlane(v.wg_p[i]);
     if (p < 0) return;  // no work left for this workgroup
@@ -781,7 +792,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   bool first = true, deferred = false, replay = false;
   int d_p = 0, d_kvh = 0;
   for (;;) {
-    int nt = grid_nt, t0 = 0, t1 = grid_nt;
+    int nt = grid_nt, t0 = grid_t0, t1 = grid_nt;
     bool last = true;
     if (balanced) {
       nt = __builtin_amdgcn_readfirstlane(v.pair_nt[p]);
@@ -806,7 +817,8 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     }
     if (go) {
       run_unit(t0, t1);
-      if (t0 == 0 && t1 == nt) store_final();
+      // Per-unit workgroups store their rows (a key split's unnormalised part, into its slot).
+      if (!balanced || (t0 == 0 && t1 == nt)) store_final();
       else store_partial((int64_t(i) * 2 + (slot0 ? 0 : 1)) * ROWS);
       first = false;
     }
@@ -993,7 +1005,8 @@ int launch_prefill(const PrefillArgs& a, int batch, int max_q, hipStream_t s) {
   const auto kern = a.page_shift >= 0 ? prefill_kernel<D, BAL, true, Tag>()
                                       : prefill_kernel<D, BAL, false, Tag>();
   if constexpr (!BAL) {
-    const dim3 grid(unsigned(a.hkv), unsigned(ceil_div(max_q, a.tq)), unsigned(batch));
+    const dim3 grid(unsigned(a.hkv), unsigned(ceil_div(max_q, a.tq)),
+                    unsigned(batch * a.key_splits));
     hipLaunchKernelGGL(kern, grid, dim3(64 * S::W), 0, s, a);
     return check_launch("ti_gqa_prefill_paged");
   } else {
@@ -1071,7 +1084,7 @@ int prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h, const v
                   int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                   int64_t num_blocks, int32_t max_blocks_per_seq, int32_t causal, int32_t dtype,
                   void* stream, const void* gate, int64_t gate_stride_t, int64_t gate_stride_h,
-                  float* uo = nullptr, float* uml = nullptr) {
+                  float* uo = nullptr, float* uml = nullptr, int32_t key_splits = 1) {
   if (dtype != TI_DTYPE_BF16 && dtype != TI_DTYPE_F16) {
     return fail(TI_EUNSUPPORTED, "ti_gqa_prefill_paged: dtype code %d is not bf16/fp16", dtype);
   }
@@ -1091,6 +1104,11 @@ int prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h, const v
   if (page_size <= 0 || page_size % 16 != 0) {
     return fail(TI_EUNSUPPORTED, "ti_gqa_prefill_paged: page_size %d not a multiple of 16",
                 page_size);
+  }
+  if (key_splits < 1 || (key_splits > 1 && (workspace != nullptr || uo == nullptr)) ||
+      int64_t(batch) * key_splits > 65535) {
+    return fail(TI_EINVAL, "ti_gqa_prefill_paged_partial: key_splits %d needs the unnormalised "
+                           "output, no workspace and batch * key_splits <= 65535", key_splits);
   }
   if (batch == 0 || total_q == 0 || max_seqlen_q == 0) return TI_OK;
   if (!q || !k_cache || !v_cache || !block_table || !cu_seqlens_q || !seqlen_k ||
@@ -1150,6 +1168,7 @@ int prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h, const v
   a.gate_sh = gate_stride_h;
   a.uo = uo;
   a.uml = uml;
+  a.key_splits = key_splits;
   if (balanced) {
     const int wgs = head_dim == 256 ? (bf16 ? balanced_wgs<256, Bf16>() : balanced_wgs<256, F16>())
                                     : (bf16 ? balanced_wgs<128, Bf16>() : balanced_wgs<128, F16>());
@@ -1231,7 +1250,7 @@ extern "C" int ti_gqa_prefill_paged_partial(
     void* workspace, int64_t workspace_bytes, int32_t batch, int32_t total_q,
     int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
     int32_t page_size, int64_t num_blocks, int32_t max_blocks_per_seq, int32_t causal,
-    int32_t dtype, void* stream) {
+    int32_t dtype, int32_t key_splits, void* stream) {
   if (!o_part || !ml_part) {
     return ti::fail(TI_EINVAL, "ti_gqa_prefill_paged_partial: null output pointer");
   }
@@ -1239,5 +1258,27 @@ extern "C" int ti_gqa_prefill_paged_partial(
                            block_table_stride, cu_seqlens_q, seqlen_k, nullptr, 0, 0, workspace,
                            workspace_bytes, batch, total_q, max_seqlen_q, num_q_heads,
                            num_kv_heads, head_dim, page_size, num_blocks, max_blocks_per_seq,
-                           causal, dtype, stream, nullptr, 0, 0, o_part, ml_part);
+                           causal, dtype, stream, nullptr, 0, 0, o_part, ml_part, key_splits);
+}
+
+// Key splits of a one-sequence partial pass of `total_q` queries over `kv_tokens` keys (the shared
+// prefix of a decode batch): enough (query block, KV head, key range) workgroups to give every CU
+// one, each range at least kMinSplitTiles key tiles.
+extern "C" int32_t ti_gqa_prefill_key_splits(int32_t total_q, int32_t num_q_heads,
+                                             int32_t num_kv_heads, int32_t head_dim,
+                                             int32_t kv_tokens) {
+  using namespace ti;
+  constexpr int kMinSplitTiles = 4;
+  if (total_q <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || kv_tokens <= 0 ||
+      (head_dim != 128 && head_dim != 256)) {
+    return 1;
+  }
+  const int64_t tq = prefill_rows(head_dim, false) / (num_q_heads / num_kv_heads);
+  if (tq <= 0) return 1;
+  const int64_t units = int64_t(num_kv_heads) * ceil_div(total_q, tq);
+  const int64_t tiles = ceil_div(kv_tokens, prefill_key_tile(head_dim, false));
+  int64_t s = device_cu_count() / units;
+  s = s < ceil_div(tiles, kMinSplitTiles) ? s : ceil_div(tiles, kMinSplitTiles);
+  s = s < 65535 ? s : 65535;
+  return int32_t(s > 1 ? s : 1);
 }

@@ -44,6 +44,14 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
     return s.value, m.value, w.value
 
 
+@functools.lru_cache(maxsize=256)
+def _prefix_splits(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                   prefix_tokens: int) -> int:
+    """Key ranges the shared-prefix pass is cut into (host-known sizes only)."""
+    return int(_lib.load().ti_gqa_prefill_key_splits(batch, num_q_heads, num_kv_heads, head_dim,
+                                                     prefix_tokens))
+
+
 _STATIC_I32: dict = {}
 
 
@@ -175,18 +183,17 @@ def gqa_decode_paged_fn(
                              f"{page_size} within the block table's {width} pages")
         if variant == "scalar":
             raise ValueError("shared_prefix_tokens needs the MFMA variant")
-        from .gqa_prefill_paged import _workspace_bytes
-        pre_o = torch.empty((b, h_q, d), dtype=torch.float32, device=dev)
-        pre_ml = torch.empty((b, h_q, 2), dtype=torch.float32, device=dev)
-        pws_bytes = _workspace_bytes(1, b, h_q, h_kv, d, page_size, prefix // page_size)
-        pws = torch.empty(pws_bytes, dtype=torch.uint8, device=dev) if pws_bytes > 0 else None
-        # The batch's queries as the B "tokens" of one non-causal chunk over sequence 0's prefix.
+        # The batch's queries as the B "tokens" of one non-causal chunk over sequence 0's prefix,
+        # its keys cut into `splits` ranges, each range's unnormalised part merged by the decode.
+        splits = _prefix_splits(b, h_q, h_kv, d, prefix)
+        pre_o = torch.empty((splits, b, h_q, d), dtype=torch.float32, device=dev)
+        pre_ml = torch.empty((splits, b, h_q, 2), dtype=torch.float32, device=dev)
         _lib.check(lib.ti_gqa_prefill_paged_partial(
             q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
             block_table.data_ptr(), block_table.stride(0), _static_i32((0, b), dev).data_ptr(),
             _static_i32((prefix,), dev).data_ptr(), pre_o.data_ptr(), pre_ml.data_ptr(),
-            pws.data_ptr() if pws is not None else None, pws_bytes, 1, b, b, h_q, h_kv, d,
-            page_size, rows // page_size, prefix // page_size, 0, code, _lib.stream_handle(dev)))
+            None, 0, 1, b, b, h_q, h_kv, d, page_size, rows // page_size, prefix // page_size, 0,
+            code, splits, _lib.stream_handle(dev)))
         width -= prefix // page_size
     _, _, ws_bytes = decode_plan(b, h_q, h_kv, d, page_size, width, split_tokens)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
@@ -207,8 +214,8 @@ def gqa_decode_paged_fn(
     if prefix:
         _lib.check(lib.ti_gqa_decode_paged_prefixed(
             *args, g3.data_ptr() if g3 is not None else None, g3.stride(0) if g3 is not None else 0,
-            g3.stride(1) if g3 is not None else 0, pre_o.data_ptr(), pre_ml.data_ptr(), prefix,
-            _lib.stream_handle(dev)))
+            g3.stride(1) if g3 is not None else 0, pre_o.data_ptr(), pre_ml.data_ptr(), splits,
+            prefix, _lib.stream_handle(dev)))
         return out
     if gate is None:
         _lib.check(lib.ti_gqa_decode_paged(*args, _lib.stream_handle(dev)))
