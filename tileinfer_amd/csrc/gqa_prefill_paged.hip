@@ -470,7 +470,8 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     }
   };
 
-  auto compute = [&](const uint16_t* sk, const uint16_t* sv, uint32_t empty, int k0)
+  // Q.K^T of the tile at k0 (stage sk), the online softmax, and P^T in MFMA operand form.
+  auto qk_softmax = [&](const uint16_t* sk, uint32_t empty, int k0, u32x4 (&pop)[C][NS / 2])
       __attribute__((always_inline)) {
     // S^T of each sub-tile that holds a key some row of the wave can see; the rest stay zero.
     f32x4 s[NS][C];
@@ -517,7 +518,6 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     bool full = k0 + kKT - 1 <= wave_first_key;
 #pragma unroll
     for (int j = 0; j < NS; ++j) full = full && rows[j] == 16;
-    u32x4 pop[C][NS / 2];
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       float v[4 * NS];
@@ -572,6 +572,11 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
         }
       }
     }
+  };
+
+  // O += P.V of the tile at k0 (stage sv), with P^T from qk_softmax.
+  auto pv = [&](const uint16_t* sv, int k0, const u32x4 (&pop)[C][NS / 2])
+      __attribute__((always_inline)) {
     // O^T[16 d x 16 rows] += V^T[16 d x 32 keys] . P^T[32 keys x 16 rows] per pair of sub-tiles,
     // d-tile dt covering d = 16 dt .. 16 dt + 15; the A operand comes from two transposed reads.
     // The reads run two d-tiles ahead of the MFMAs; the scheduling barriers keep that order (left
@@ -608,6 +613,13 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
         }
       }
     }
+  };
+
+  auto compute = [&](const uint16_t* sk, const uint16_t* sv, uint32_t empty, int k0)
+      __attribute__((always_inline)) {
+    u32x4 pop[C][NS / 2];
+    qk_softmax(sk, empty, k0, pop);
+    pv(sv, k0, pop);
   };
 
   // Attention of unit (b, kvh, qb0) over its key tiles [t0, t1): leaves the unnormalised o and
