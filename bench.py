@@ -493,6 +493,47 @@ def metric_extras(kv, tables, seqlen, q, dev, args) -> dict:
                                                2)})
         ctx *= 2
     res["decode_ctx_sweep_batch64"] = sweep
+    res["other_configs"] = other_configs_decode(dev, args)
+    return res
+
+
+def other_configs_decode(dev, args) -> dict:
+    """One decode launch of BASELINE configs 2, 4 and 5 at their stated sizes (their own seeded
+    caches, separate from the config-3 slab), timed with HIP events; config 2 is also checked
+    against the CPU oracle, config 5 is timed both plain (cache-keeping policy) and with
+    shared_prefix_tokens=8192."""
+    from oracle.ref_torch import ref_gqa_decode_paged
+    from tileinfer_amd import workloads as wl
+
+    res = {}
+    for cfg in (2, 4, 5):
+        st = {2: wl.config2, 4: lambda device: wl.config4(device=device)[0],
+              5: wl.config5}[cfg](device=dev)
+        ctx = st.seqlen.tolist()
+        nbytes = decode_bytes(ctx)
+        call = functools.partial(gqa_decode_paged_fn, st.q, st.k_cache, st.v_cache,
+                                 st.block_table, st.seqlen, BLOCK, kv_reuse=cfg == 5)
+        us = _time(call, args.steps, args.warmup)
+        entry = {"batch": len(ctx), "ctx_sum": sum(ctx), "decode_us": round(us, 2),
+                 "decode_GBps_algorithmic": round(nbytes / (us * 1e-6) / 1e9, 1),
+                 "decode_pct_of_peak_hbm": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 2)}
+        if cfg == 2:
+            out = call()
+            ref = ref_gqa_decode_paged(st.q.cpu(), st.k_cache.cpu(), st.v_cache.cpu(),
+                                       st.block_table.cpu(), st.seqlen.cpu(), BLOCK).float()
+            err = (out.float().cpu() - ref).abs()
+            entry["decode_within_tol"] = bool((err <= 2e-2 + 1e-2 * ref.abs()).all())
+            entry["decode_max_abs_err"] = round(float(err.max()), 6)
+        if cfg == 5:
+            pre = functools.partial(gqa_decode_paged_fn, st.q, st.k_cache, st.v_cache,
+                                    st.block_table, st.seqlen, BLOCK,
+                                    shared_prefix_tokens=st.meta["prefix_tokens"])
+            entry["decode_us_shared_prefix"] = round(_time(pre, args.steps, args.warmup), 2)
+            entry["note"] = ("plain decode with the cache-keeping policy (shared prefix pages hit "
+                             "L2/MALL, so the logical % can exceed 100); shared_prefix: the "
+                             "8,192-token prefix attended once for the batch")
+        res[f"config{cfg}"] = entry
+        del st
     return res
 
 

@@ -143,5 +143,13 @@ def dtype_code(dtype: torch.dtype) -> int:
     raise TypeError(f"unsupported dtype {dtype}: the paged KV path handles bfloat16 and float16")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on `device` (torch's raw query when it has one:
+    ~0.1 us against ~2 us for building a torch.cuda.Stream object)."""
+    if _raw_stream is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(index)
     return torch.cuda.current_stream(device).cuda_stream
