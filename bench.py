@@ -494,6 +494,34 @@ def metric_extras(kv, tables, seqlen, q, dev, args) -> dict:
         ctx *= 2
     res["decode_ctx_sweep_batch64"] = sweep
     res["other_configs"] = other_configs_decode(dev, args)
+    res["prefill_config4"] = prefill_extras(dev, args)
+    return res
+
+
+def prefill_extras(dev, args) -> dict:
+    """Config 4's paged prefill attention on its own seeded pages (the `--config 4` run times the
+    same calls on the pages its append wrote): the 2,048-token first chunk (causal over itself)
+    and a 2,048-token continuation over 6,144 cached tokens, with the default schedule and each
+    schedule forced; HIP events on the launch stream."""
+    from tileinfer_amd import workloads as wl
+    from tileinfer_amd.kernels.gqa_prefill_paged import gqa_prefill_paged_fn
+
+    res = {}
+    for name, cached in (("first_chunk", 0), ("continuation", 6144)):
+        w = wl.config4_prefill(device=dev, cached=cached)
+        q_len, kv_len = int(w.q.shape[0]), int(w.seqlen_k[0])
+        times = _time_interleaved(
+            [functools.partial(gqa_prefill_paged_fn, w.q, w.k_cache, w.v_cache, w.block_table,
+                               w.cu_seqlens_q, w.seqlen_k, q_len, schedule=sc,
+                               max_seqlen_k=kv_len) for sc in ("auto", "balanced", "per_unit")],
+            args.steps, args.warmup)
+        flops = w.flops()
+        res[name] = {"q_len": q_len, "kv_len": kv_len, "flops": flops,
+                     "us": round(times[0], 2),
+                     "TFLOPs": round(flops / (times[0] * 1e-6) / 1e12, 1),
+                     "pct_of_peak_bf16_dense": round(100 * flops / (times[0] * 1e-6) / 2.5e15, 1),
+                     "balanced_us": round(times[1], 2), "per_unit_us": round(times[2], 2)}
+        del w
     return res
 
 
