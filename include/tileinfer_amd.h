@@ -330,6 +330,32 @@ int ti_gqa_decode_paged_gated(const void* q, int64_t q_stride_b, int64_t q_strid
                               void* stream);
 
 /*
+ * The decode step's append and attention in one call: ti_kv_append of one new token per sequence
+ * (key/value row b [num_kv_heads * head_dim] at key_row_stride / value_row_stride elements, written
+ * to cache row slot_mapping[b]; rows with a slot < 0 or >= num_slots are skipped) followed by
+ * ti_gqa_decode_paged, bitwise what the two calls give, in the launches of the decode alone: the
+ * workgroup whose tokens end at a sequence's last position writes that token's rows before it
+ * reads them. Requires slot_mapping[b] to be the slot of position seqlen[b] - 1 (the reference
+ * runner's decode step: engine/model_runner.py:628-637 with context_lens = num_tokens), so the
+ * rows written are the rows the call reads. Cache rows are the decode's token rows
+ * ([num_blocks * page_size, num_kv_heads * head_dim]). MFMA variant only.
+ * Reference counterpart: store_kvcache(k, v, k_cache, v_cache, slot_mapping) then
+ * gqa_decode_paged_fn(q, k_cache, v_cache, block_table, seqlen_kv) (model/qwen_36.py:1018, 1074;
+ * kernels/kvcache_store.py:43-71, kernels/gqa_decode_paged.py:392-437).
+ */
+int ti_gqa_decode_paged_append(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                               const void* k_cache, const void* v_cache,
+                               const int32_t* block_table, int64_t block_table_stride,
+                               const int32_t* seqlen, void* out, void* workspace,
+                               int64_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                               int64_t num_blocks, int32_t max_blocks_per_seq,
+                               int32_t split_tokens, int32_t variant, int32_t dtype,
+                               const void* key, const void* value, int64_t key_row_stride,
+                               int64_t value_row_stride, const int32_t* slot_mapping,
+                               int64_t num_slots, void* stream);
+
+/*
  * ti_gqa_decode_paged (optionally gated) for a batch whose sequences share their first
  * prefix_tokens tokens (a multiple of page_size): the kernel attends to tokens
  * [prefix_tokens, seqlen[b]) of each sequence, through block_table columns from

@@ -25,7 +25,7 @@ TI_DECODE_AUTO = 0
 TI_DECODE_MFMA = 1
 TI_DECODE_SCALAR = 2
 TI_DECODE_REUSE_KV = 0x10
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # Every symbol declared in include/tileinfer_amd.h, with its ctypes signature.
 _c_i32, _c_i64, _c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
@@ -76,6 +76,11 @@ SIGNATURES = {
                                              _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                              ctypes.c_float, _c_i32, _c_vp]),
     "ti_sigmoid_mul": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i32, _c_vp]),
+    "ti_gqa_decode_paged_append": (ctypes.c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp,
+                                                  _c_i64, _c_vp, _c_vp, _c_vp, _c_i64, _c_i32,
+                                                  _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32,
+                                                  _c_i32, _c_i32, _c_i32, _c_vp, _c_vp, _c_i64,
+                                                  _c_i64, _c_vp, _c_i64, _c_vp]),
     "ti_gqa_decode_paged_gated": (ctypes.c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_i64,
                                                  _c_vp, _c_vp, _c_vp, _c_i64, _c_i32, _c_i32,
                                                  _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32,

@@ -51,4 +51,4 @@ int device_cu_count() {
 
 extern "C" const char* ti_last_error(void) { return ti::g_last_error; }
 
-extern "C" int32_t ti_abi_version(void) { return 6; }
+extern "C" int32_t ti_abi_version(void) { return 7; }

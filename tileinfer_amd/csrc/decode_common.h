@@ -131,6 +131,16 @@ struct DecodeArgs {
   const float* pre_ml;
   int32_t pre_parts;
   int32_t ctx_offset;
+  // Optional fused append (one new token per sequence, its K/V rows not yet in the cache): row b
+  // of app_k / app_v ([B][hkv * D] at row strides app_k_sb / app_v_sb elements) is written to
+  // cache row app_slot[b] (skipped when negative or >= app_num_slots) before it is read, by the
+  // workgroup whose tiles end at the sequence's last token (the merge for sequences with none).
+  // The caller guarantees that app_slot[b] is the slot of position seqlen[b] - 1. nullptr: none.
+  const uint16_t* app_k;
+  const uint16_t* app_v;
+  int64_t app_k_sb, app_v_sb;
+  const int32_t* app_slot;
+  int64_t app_num_slots;
 };
 
 

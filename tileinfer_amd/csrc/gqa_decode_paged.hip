@@ -181,6 +181,21 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
   auto run_partition = [&](int b, int t0, int t1) {
     tok0 = t0;
     tok1 = t1;
+    // Fused append: the partition that ends at the sequence's last token writes that token's K/V
+    // rows (this wave's KV head) before any of its tiles is loaded. Its own later loads of the
+    // row then see them (the stores are waited for below, before the first tile load); no other
+    // workgroup reads that row.
+    const bool appended = a.app_slot != nullptr && t1 == seq_len(a, b);
+    if (appended) {
+      const int slot = __builtin_amdgcn_readfirstlane(a.app_slot[b]);
+      if (slot >= 0 && slot < a.app_num_slots && lane < D / 8) {  // uniform slot test
+        const int64_t dst = int64_t(slot) * a.row_stride + kvh * D + 8 * lane;
+        const u32x4 kw = load16(a.app_k + b * a.app_k_sb + kvh * D + 8 * lane);
+        const u32x4 vw = load16(a.app_v + b * a.app_v_sb + kvh * D + 8 * lane);
+        *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.k_cache) + dst) = kw;
+        *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.v_cache) + dst) = vw;
+      }
+    }
     const int page0 = tok0 / a.page_size;
     // The plan keeps every partition within kMaxSplitPages pages; the clamp only guards LDS.
     const int npages = tok1 > tok0 ? min((tok1 - 1) / a.page_size - page0 + 1, kMaxSplitPages) : 0;
@@ -199,6 +214,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     for (int t = 0; t < NT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     m_run = -INFINITY;
     l_run = 0.f;
+    if (appended) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the appended rows are written
     // Two tiles in flight: the next tile's loads are issued before the current one is consumed.
     const int ntiles = (tok1 - tok0 + 15) / 16;
     if (ntiles > 0) {
@@ -435,6 +451,18 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
     slot0 = (int64_t(b) * a.hq + h) * a.max_splits;
   } else {
     const int nb = seq_tiles(a, b);
+    if (nb == 0 && h == 0 && a.app_slot != nullptr) {
+      // Fused append of a sequence no partial workgroup covers: its whole K/V row, here.
+      const int slot = a.app_slot[b];
+      if (slot >= 0 && slot < a.app_num_slots) {
+        for (int64_t e = 8 * lane; e < a.row_stride; e += 8 * 64) {
+          *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.k_cache) + slot * a.row_stride + e) =
+              load16(a.app_k + b * a.app_k_sb + e);
+          *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.v_cache) + slot * a.row_stride + e) =
+              load16(a.app_v + b * a.app_v_sb + e);
+        }
+      }
+    }
     if (nb == 0) {  // no token of this kernel's range: zeros, or the prefix parts alone
       float e[PER];
 #pragma unroll
@@ -683,7 +711,10 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
                  int32_t split_tokens, int32_t variant, int32_t dtype, const void* gate,
                  int64_t gate_stride_b, int64_t gate_stride_h, void* stream,
                  const float* pre_o = nullptr, const float* pre_ml = nullptr,
-                 int32_t prefix_tokens = 0, int32_t prefix_parts = 0) {
+                 int32_t prefix_tokens = 0, int32_t prefix_parts = 0,
+                 const void* app_key = nullptr, const void* app_value = nullptr,
+                 int64_t app_key_stride = 0, int64_t app_value_stride = 0,
+                 const int32_t* app_slot = nullptr, int64_t app_num_slots = 0) {
   if (dtype != TI_DTYPE_BF16 && dtype != TI_DTYPE_F16) {
     return fail(TI_EUNSUPPORTED, "ti_gqa_decode_paged: dtype code %d is not bf16/fp16", dtype);
   }
@@ -764,6 +795,28 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
   if (pre_o != nullptr && kind == TI_DECODE_SCALAR) {
     return fail(TI_EUNSUPPORTED, "ti_gqa_decode_paged_prefixed: MFMA variant only");
   }
+  a.app_k = static_cast<const uint16_t*>(app_key);
+  a.app_v = static_cast<const uint16_t*>(app_value);
+  a.app_k_sb = app_key_stride;
+  a.app_v_sb = app_value_stride;
+  a.app_slot = app_slot;
+  a.app_num_slots = app_num_slots;
+  if (app_slot != nullptr) {
+    const int64_t row = a.row_stride;
+    if (kind == TI_DECODE_SCALAR) {
+      return fail(TI_EUNSUPPORTED, "ti_gqa_decode_paged_append: MFMA variant only");
+    }
+    if (!app_key || !app_value || app_num_slots < 0 || app_key_stride < row ||
+        app_value_stride < row || app_key_stride % 8 || app_value_stride % 8 ||
+        (reinterpret_cast<uintptr_t>(app_key) & 15) ||
+        (reinterpret_cast<uintptr_t>(app_value) & 15)) {
+      return fail(TI_EINVAL,
+                  "ti_gqa_decode_paged_append: key/value must be 16-byte aligned rows of at least "
+                  "%lld elements (row strides %lld, %lld), num_slots %lld",
+                  (long long)row, (long long)app_key_stride, (long long)app_value_stride,
+                  (long long)app_num_slots);
+    }
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf16 = dtype == TI_DTYPE_BF16;
   if (kind == TI_DECODE_SCALAR) {
@@ -805,6 +858,23 @@ extern "C" int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_
                           block_table_stride, seqlen, out, workspace, workspace_bytes, batch,
                           num_q_heads, num_kv_heads, head_dim, page_size, num_blocks,
                           max_blocks_per_seq, split_tokens, variant, dtype, nullptr, 0, 0, stream);
+}
+
+extern "C" int ti_gqa_decode_paged_append(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache, const void* v_cache,
+    const int32_t* block_table, int64_t block_table_stride, const int32_t* seqlen, void* out,
+    void* workspace, int64_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_blocks,
+    int32_t max_blocks_per_seq, int32_t split_tokens, int32_t variant, int32_t dtype,
+    const void* key, const void* value, int64_t key_row_stride, int64_t value_row_stride,
+    const int32_t* slot_mapping, int64_t num_slots, void* stream) {
+  if (!slot_mapping) return ti::fail(TI_EINVAL, "ti_gqa_decode_paged_append: null slot_mapping");
+  return ti::decode_entry(q, q_stride_b, q_stride_h, k_cache, v_cache, block_table,
+                          block_table_stride, seqlen, out, workspace, workspace_bytes, batch,
+                          num_q_heads, num_kv_heads, head_dim, page_size, num_blocks,
+                          max_blocks_per_seq, split_tokens, variant, dtype, nullptr, 0, 0, stream,
+                          nullptr, nullptr, 0, 0, key, value, key_row_stride, value_row_stride,
+                          slot_mapping, num_slots);
 }
 
 // ---- No-allocation entry point -----------------------------------------------------------------

@@ -52,6 +52,31 @@ def _prefix_splits(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: in
                                                      prefix_tokens))
 
 
+def _append_rows(append, b: int, h_kv: int, d: int, dt, dev):
+    """The append= operands checked as store_kvcache checks them: key/value as [B, H_kv * D] rows
+    (16-byte aligned, unit element stride; copied only if they are not) and slot_mapping as a
+    contiguous [B] int32 tensor."""
+    if not isinstance(append, (tuple, list)) or len(append) != 3:
+        raise ValueError("append must be (key, value, slot_mapping)")
+    key, value, slots = append
+    row = h_kv * d
+    for name, t in (("key", key), ("value", value)):
+        if not isinstance(t, torch.Tensor) or t.numel() != b * row or t.shape[0] != b:
+            raise ValueError(f"append {name} must hold [{b}, {h_kv}, {d}] values")
+        if t.dtype != dt or t.device != dev:
+            raise ValueError(f"append {name} must be {dt} on {dev}")
+    if (not isinstance(slots, torch.Tensor) or slots.dtype != torch.int32 or slots.dim() != 1
+            or slots.shape[0] != b or slots.device != dev):
+        raise ValueError(f"append slot_mapping must be [{b}] int32 on {dev}")
+    flat = []
+    for t in (key, value):
+        f = t.reshape(b, row)
+        if f.stride(1) != 1 or f.stride(0) % 8 or f.data_ptr() % 16:
+            f = f.contiguous()
+        flat.append(f)
+    return flat[0], flat[1], slots.contiguous()
+
+
 _STATIC_I32: dict = {}
 
 
@@ -134,6 +159,7 @@ def gqa_decode_paged_fn(
     kv_reuse: bool = False,
     gate: torch.Tensor | None = None,
     shared_prefix_tokens: int = 0,
+    append: tuple | None = None,
 ) -> torch.Tensor:
     """Single-query paged GQA attention.
 
@@ -162,11 +188,21 @@ def gqa_decode_paged_fn(
             tokens [P, seqlen) of each sequence and merges the two parts. Within the decode
             tolerance of the plain call; bitwise the same for shared and private prefix pages.
             MFMA variant only.
+        append: keyword-only ``(key, value, slot_mapping)``, the decode step's new token per
+            sequence (key/value [B, H_kv, D] in q's dtype, slot_mapping [B] int32 with
+            slot_mapping[b] the slot of position seqlen_kv[b] - 1, or -1 to skip): written into
+            the cache inside this call, bitwise what ``store_kvcache(key, value, k_cache rows,
+            v_cache rows, slot_mapping)`` before the decode gives (model/qwen_36.py:1018, 1074),
+            without the append's launch. Not combined with ``gate``, ``shared_prefix_tokens`` or
+            the scalar variant.
     Returns:
         [B, H_q, D] tensor in q's dtype.
     """
     q, block_table, seqlen_kv, (b, h_q, d, h_kv, rows, page_size, dt, code, dev) = _checked(
         q, k_cache, v_cache, block_table, seqlen_kv, page_size, variant)
+    if append is not None and (gate is not None or shared_prefix_tokens or variant == "scalar"):
+        raise ValueError("append= combines with neither gate=, shared_prefix_tokens= nor the "
+                         "scalar variant")
     if out is None:
         out = torch.empty((b, h_q, d), dtype=dt, device=dev)
     elif (out.shape != (b, h_q, d) or out.dtype != dt or out.device != dev
@@ -216,6 +252,12 @@ def gqa_decode_paged_fn(
             *args, g3.data_ptr() if g3 is not None else None, g3.stride(0) if g3 is not None else 0,
             g3.stride(1) if g3 is not None else 0, pre_o.data_ptr(), pre_ml.data_ptr(), splits,
             prefix, _lib.stream_handle(dev)))
+        return out
+    if append is not None:
+        kf, vf, slots = _append_rows(append, b, h_kv, d, dt, dev)
+        _lib.check(lib.ti_gqa_decode_paged_append(
+            *args, kf.data_ptr(), vf.data_ptr(), kf.stride(0), vf.stride(0), slots.data_ptr(),
+            rows, _lib.stream_handle(dev)))
         return out
     if gate is None:
         _lib.check(lib.ti_gqa_decode_paged(*args, _lib.stream_handle(dev)))
