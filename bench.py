@@ -521,8 +521,46 @@ def prefill_extras(dev, args) -> dict:
                      "TFLOPs": round(flops / (times[0] * 1e-6) / 1e12, 1),
                      "pct_of_peak_bf16_dense": round(100 * flops / (times[0] * 1e-6) / 2.5e15, 1),
                      "balanced_us": round(times[1], 2), "per_unit_us": round(times[2], 2)}
+        if cached == 0:
+            res["torch_sdpa_flash"] = {"first_chunk_causal": _sdpa_flash_us(w, True, args)}
+        else:
+            ours = _time(functools.partial(gqa_prefill_paged_fn, w.q, w.k_cache, w.v_cache,
+                                           w.block_table, w.cu_seqlens_q, w.seqlen_k, q_len,
+                                           causal=False, max_seqlen_k=kv_len),
+                         args.steps, args.warmup)
+            nc = wl.prefill_flops([q_len], [kv_len], causal=False)
+            res["torch_sdpa_flash"]["noncausal_2048x8192"] = _sdpa_flash_us(w, False, args)
+            res["noncausal_2048x8192"] = {"us": round(ours, 2), "flops": nc,
+                                          "TFLOPs": round(nc / (ours * 1e-6) / 1e12, 1)}
         del w
     return res
+
+
+def _sdpa_flash_us(w, causal: bool, args) -> dict:
+    """The vendor reference point: torch.nn.functional.scaled_dot_product_attention with the
+    flash backend forced (PyTorch-ROCm's prebuilt kernels) on the same queries over the step's K/V
+    gathered into dense [1, H_q, S, D] tensors (K/V heads expanded to the 24 query heads), top-left
+    causal mask (equal to the bottom-right one when S_q = S_k)."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from tileinfer_amd import workloads as wl
+
+    q_len, kv_len = int(w.q.shape[0]), int(w.seqlen_k[0])
+    if causal and q_len != kv_len:
+        return {"us": None, "note": "top-left mask differs from the call's"}
+    pos = torch.arange(kv_len, device=w.q.device)
+    blocks = w.block_table[0, pos // BLOCK].long()
+    dense = lambda c: c[blocks, pos % BLOCK].permute(1, 0, 2).repeat_interleave(  # noqa: E731
+        HQ // HKV, dim=0).unsqueeze(0).contiguous()
+    k, v = dense(w.k_cache), dense(w.v_cache)
+    q = w.q.permute(1, 0, 2).unsqueeze(0).contiguous()
+    flops = wl.prefill_flops([q_len], [kv_len], causal=causal)
+    try:
+        with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+            us = _time(lambda: torch.nn.functional.scaled_dot_product_attention(
+                q, k, v, is_causal=causal), args.steps, args.warmup)
+    except RuntimeError as e:
+        return {"us": None, "note": f"flash backend unavailable: {str(e)[:100]}"}
+    return {"us": round(us, 2), "TFLOPs": round(flops / (us * 1e-6) / 1e12, 1)}
 
 
 def other_configs_decode(dev, args) -> dict:
