@@ -114,3 +114,36 @@ def test_fused_append_rejects(dev):
         gqa_decode_paged_fn(q, kc, vc, table, seqlen, append=(app[0][:1], app[1], app[2]))
     with pytest.raises(ValueError):
         gqa_decode_paged_fn(q, kc, vc, table, seqlen, append=(app[0], app[1], app[2].long()))
+
+
+def test_fused_append_graph_capture_replay(dev):
+    """The fused call captured in a HIP graph: three replays, each after new q / key / value
+    contents and an eager call between, equal the eager store_kvcache + decode of that data."""
+    step = config2()
+    say("decode append fused graph replay")
+    q, kn, vn = step.q.to(dev), step.k_new.to(dev), step.v_new.to(dev)
+    table, seqlen, slot = step.block_table.to(dev), step.seqlen.to(dev), step.slot_mapping.to(dev)
+    kc, vc = step.k_cache.to(dev), step.v_cache.to(dev)
+    out = torch.empty_like(q)
+    call = lambda: gqa_decode_paged_fn(q, kc, vc, table, seqlen, step.page_size,  # noqa: E731
+                                       out=out, append=(kn, vn, slot))
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    gen = torch.Generator(device=dev).manual_seed(36)
+    for rep in range(3):
+        for t in (q, kn, vn):
+            t.copy_(torch.randn(t.shape, generator=gen, device=dev).to(t.dtype))
+        kr, vr = kc.clone(), vc.clone()
+        store_kvcache(kn, vn, flat(kr), flat(vr), slot)
+        ref = gqa_decode_paged_fn(q, kr, vr, table, seqlen, step.page_size)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(out), bits(ref)), f"replay {rep}"
+        assert torch.equal(bits(kc), bits(kr)) and torch.equal(bits(vc), bits(vr)), f"replay {rep}"
