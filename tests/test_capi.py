@@ -215,3 +215,25 @@ def test_hbm_probe_rejects_partial_sweeps():
     assert lib.ti_hbm_read_probe(fake + 8, fake, None, 4, 4096, 4, 1, 1, 8, fake,
                                  None) == _lib.TI_EINVAL
     assert lib.ti_hbm_read_probe(None, None, None, 0, 4096, 0, 1, 1, 8, None, None) == _lib.TI_OK
+
+
+def test_fused_append_decode_argument_errors_without_device():
+    """ti_gqa_decode_paged_append refuses bad append operands on the host, before anything is
+    launched (stand-in device addresses, never dereferenced: every call below fails first)."""
+    lib = _lib.load()
+    s, m, w = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    _lib.check(lib.ti_gqa_decode_plan(2, 24, 4, 256, 16, 8, 0, ctypes.byref(s), ctypes.byref(m),
+                                      ctypes.byref(w)))
+    fake = 1 << 20  # 16-byte aligned stand-in address
+    nb, rows = 16, 16 * 16
+
+    def call(key=fake, stride=1024, slots=fake, num_slots=rows, variant=0):
+        return lib.ti_gqa_decode_paged_append(
+            fake, 24 * 256, 256, fake, fake, fake, 8, fake, fake, fake, w.value, 2, 24, 4, 256,
+            16, nb, 8, 0, variant, 0, key, fake, stride, 1024, slots, num_slots, None)
+
+    assert call(slots=None) == _lib.TI_EINVAL and b"slot_mapping" in lib.ti_last_error()
+    assert call(num_slots=rows + 1) == _lib.TI_EINVAL and b"num_slots" in lib.ti_last_error()
+    assert call(key=fake + 8) == _lib.TI_EINVAL and b"aligned" in lib.ti_last_error()
+    assert call(stride=1000) == _lib.TI_EINVAL
+    assert call(variant=_lib.TI_DECODE_SCALAR) == _lib.TI_EUNSUPPORTED

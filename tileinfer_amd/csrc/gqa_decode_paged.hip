@@ -806,13 +806,14 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
     if (kind == TI_DECODE_SCALAR) {
       return fail(TI_EUNSUPPORTED, "ti_gqa_decode_paged_append: MFMA variant only");
     }
-    if (!app_key || !app_value || app_num_slots < 0 || app_key_stride < row ||
+    if (!app_key || !app_value || app_num_slots < 0 ||
+        app_num_slots > num_blocks * int64_t(page_size) || app_key_stride < row ||
         app_value_stride < row || app_key_stride % 8 || app_value_stride % 8 ||
         (reinterpret_cast<uintptr_t>(app_key) & 15) ||
         (reinterpret_cast<uintptr_t>(app_value) & 15)) {
       return fail(TI_EINVAL,
                   "ti_gqa_decode_paged_append: key/value must be 16-byte aligned rows of at least "
-                  "%lld elements (row strides %lld, %lld), num_slots %lld",
+                  "%lld elements (row strides %lld, %lld), num_slots %lld at most the cache's rows",
                   (long long)row, (long long)app_key_stride, (long long)app_value_stride,
                   (long long)app_num_slots);
     }
