@@ -407,6 +407,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
 template <int D, typename Tag>
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batch) {
   constexpr int PER = D / 64;  // d-values per thread
+  typedef float PartVec __attribute__((ext_vector_type(PER)));  // one lane's piece of a part row
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int lane = threadIdx.x;
@@ -498,11 +499,29 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
   auto part = [&](int s) -> int64_t {
     return slot0 + s * stride + ((s == 0 && first_part_slot1) ? a.hq : 0);
   };
-  // Maximum over the parts' m (and the prefix parts'), lane-parallel.
-  float m = -INFINITY;
+  // The o rows of the first kBurst parts are requested ahead of the (m, l) loads: they do not
+  // depend on the weights, so one memory latency covers both. Past nparts the last part's row is
+  // read again (a valid row) and left out of the sum. nburst is uniform; readfirstlane lets the
+  // compiler see it, so these are plain vector loads.
+  constexpr int kBurst = 16;
+  const int nburst = __builtin_amdgcn_readfirstlane(min(nparts, kBurst));
+  PartVec vb[kBurst];
+#pragma unroll
+  for (int u = 0; u < kBurst; ++u) {
+    vb[u] = *reinterpret_cast<const PartVec*>(a.part_o + part(min(u, nburst - 1)) * D + d0);
+  }
+  // Maximum over the parts' m (and the prefix parts'), lane-parallel; lane s keeps the (m, l) of
+  // part s (parts 0-63) for the weights below.
+  float m = -INFINITY, ms0 = -INFINITY, ls0 = 0.f;
   for (int s0 = 0; s0 < nparts; s0 += 64) {
     const int s = s0 + lane;
-    m = fmaxf(m, s < nparts ? a.part_ml[2 * part(s)] : -INFINITY);
+    float ms = -INFINITY;
+    if (s < nparts) {
+      ms = a.part_ml[2 * part(s)];
+      if (s0 == 0) ls0 = a.part_ml[2 * part(s) + 1];
+    }
+    if (s0 == 0) ms0 = ms;
+    m = fmaxf(m, ms);
   }
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
@@ -513,37 +532,50 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
   float l = 0.f;
   if (me != -INFINITY) l = add_pre(m, acc);  // the prefix parts first (fixed order)
   if (m != -INFINITY) {
-    // Parts in chunks of 64: lane s holds part s0+s's weight; the o rows of 8 parts are loaded
-    // back to back so their latencies overlap. Summation order is fixed (ascending part).
+    // Parts in chunks of 64: lane s holds part s0+s's weight w and w * l; part j's are broadcast
+    // when it is added. Summation order is fixed (ascending part) for o and for l.
     for (int s0 = 0; s0 < nparts; s0 += 64) {
       const int s = s0 + lane;
-      float w = 0.f, wl = 0.f;
-      if (s < nparts) {
-        const int64_t ps = part(s);
-        const float ms = a.part_ml[2 * ps];
-        w = ms == -INFINITY ? 0.f : fast_exp2(ms - m);
-        wl = w * a.part_ml[2 * ps + 1];
+      float ms = ms0, ls = ls0;
+      if (s0 > 0) {
+        ms = -INFINITY;
+        ls = 0.f;
+        if (s < nparts) {
+          ms = a.part_ml[2 * part(s)];
+          ls = a.part_ml[2 * part(s) + 1];
+        }
       }
-      const int cnt = min(64, nparts - s0);
-      for (int j0 = 0; j0 < cnt; j0 += 8) {
-        float v[8][PER];
-        float wj[8];
+      const float w = ms == -INFINITY ? 0.f : fast_exp2(ms - m);
+      const float wl = w * ls;
+      const int cnt = __builtin_amdgcn_readfirstlane(min(64, nparts - s0));
+      auto add_part = [&](int j, const PartVec& v) __attribute__((always_inline)) {
+        const float wj = __shfl(w, j, 64);
+        const float lj = __shfl(wl, j, 64);
+#pragma unroll
+        for (int q = 0; q < PER; ++q) acc[q] += wj * v[q];
+        l += lj;
+      };
+      int j0 = 0;
+      if (s0 == 0) {
+#pragma unroll
+        for (int u = 0; u < kBurst; ++u) {
+          if (u < cnt) add_part(u, vb[u]);  // uniform
+        }
+        j0 = kBurst;
+      }
+      // The rest 8 at a time, loaded back to back so that their latencies overlap.
+      for (; j0 < cnt; j0 += 8) {
+        PartVec v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          wj[u] = __shfl(w, j0 + u, 64);
-          const bool live = j0 + u < cnt;
-          const float* src = a.part_o + part(s0 + (live ? j0 + u : 0)) * D + d0;
-#pragma unroll
-          for (int q = 0; q < PER; ++q) v[u][q] = live ? src[q] : 0.f;
+          const int j = min(j0 + u, cnt - 1);
+          v[u] = *reinterpret_cast<const PartVec*>(a.part_o + part(s0 + j) * D + d0);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-#pragma unroll
-          for (int q = 0; q < PER; ++q) acc[q] += wj[u] * v[u][q];
+          if (j0 + u < cnt) add_part(j0 + u, v[u]);  // uniform
         }
       }
-      // l in the same ascending order on every lane.
-      for (int j = 0; j < cnt; ++j) l += __shfl(wl, j, 64);
     }
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
