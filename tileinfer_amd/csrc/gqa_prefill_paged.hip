@@ -437,13 +437,22 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     // registers for the whole loop and be spilled.
     int wblk = wave * LPW;
     asm volatile("" : "+s"(wblk));
-    // Byte offsets of this lane's chunk of 1 KiB block blk of the tile in K and V.
-    auto chunk_offsets = [&](int blk, uint32_t& off_k, uint32_t& off_v)
+    // Byte offsets of this lane's chunk of the wave's block i (1 KiB) of the tile in K and V. The
+    // chunk's tile row has low four bits bw | RPB i | q (bw: those of the wave's first block, a
+    // multiple of RPB LPW; q = ln / CPR; disjoint bit fields), and both swizzles are XOR-linear in
+    // those bits, so each offset is a lane term, computed once per fetch, combined with a term of
+    // i alone (an XOR-add and a scalar add per load, no 32-bit multiply).
+    const int q = ln / CPR;
+    const int slot = ln % CPR;
+    const int bw = (wblk * RPB) & 15;
+    const uint32_t lane_hi = __umul24(uint32_t(bw | q), row_bytes);
+    const uint32_t lane_k = uint32_t(slot ^ lds_swizzle(bw | q)) * 16u;
+    const uint32_t lane_v = uint32_t(slot ^ lds_swizzle_v(bw | q)) * 16u;
+    auto chunk_offsets = [&](int i, uint32_t& off_k, uint32_t& off_v)
         __attribute__((always_inline)) {
-      const int row = blk * RPB + ln / CPR;            // tile row of this lane's chunk
-      const int slot = ln % CPR;
-      off_k = uint32_t(row & 15) * row_bytes + uint32_t(slot ^ lds_swizzle(row)) * 16u;
-      off_v = uint32_t(row & 15) * row_bytes + uint32_t(slot ^ lds_swizzle_v(row)) * 16u;
+      const uint32_t ri = uint32_t(RPB * i) * row_bytes;  // uniform
+      off_k = ((lane_k ^ uint32_t(16 * lds_swizzle(RPB * i))) + lane_hi) + ri;
+      off_v = ((lane_v ^ uint32_t(16 * lds_swizzle_v(RPB * i))) + lane_hi) + ri;
     };
     if constexpr (kAsmLoads) {
       const u32x4 rk = rsrc_words(a.k_cache + base, nbytes);
@@ -452,7 +461,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       for (int i = 0; i < LPW; ++i) {
         const int blk = wblk + i;                  // 1 KiB block of the tile (uniform)
         uint32_t off_k, off_v;
-        chunk_offsets(blk, off_k, off_v);
+        chunk_offsets(i, off_k, off_v);
         load_lds16(rk, off_k, sk + blk * 512);
         load_lds16(rv, off_v, sv + blk * 512);
       }
@@ -463,7 +472,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       for (int i = 0; i < LPW; ++i) {
         const int blk = wblk + i;
         uint32_t off_k, off_v;
-        chunk_offsets(blk, off_k, off_v);
+        chunk_offsets(i, off_k, off_v);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(sk + blk * 512), 16, off_k, 0, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(sv + blk * 512), 16, off_v, 0, 0, 0);
       }
