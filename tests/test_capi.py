@@ -53,6 +53,23 @@ def test_decode_plan_sizes():
     assert _plan(8, 24, 4, 256, 16, 64, 2048)[1:] == (2048, 1, 0)
 
 
+def test_balanced_plan_one_wave_per_simd_in_whole_rounds():
+    """The balanced decode plan (no split requested; this container has no device, so the plan
+    takes MI355X's 256 CUs) gives every SIMD one KV-head wave per round: 1,024 / H_kv runs per
+    KV-head group, whatever the workgroup size. When the block ids one run may stage (1,023
+    16-token tiles at page size 16) force more runs, it takes whole extra rounds, never a partial
+    one: a partial round runs alone after the others and nearly doubles the time."""
+    for hkv, hq, d in ((4, 24, 256), (8, 32, 128), (2, 16, 128), (1, 8, 128), (2, 12, 256)):
+        rc, split, wgs, ws = _plan(64, hq, hkv, d, 16, 512, 0)  # 64 x 8k: one round
+        assert (rc, split, wgs) == (0, 0, 1024 // hkv)
+        assert ws >= wgs * 2 * hq * (d + 2) * 4
+    # 64 x 32k at 8 KV heads: 131,072 tiles in runs of at most 1,023 need 129 runs per group, one
+    # more than a round holds (128), so two whole rounds (256 runs), not 129.
+    assert _plan(64, 32, 8, 128, 16, 2048, 0)[2] == 256
+    # At 4 KV heads the same batch fits one round (256 runs of 512 tiles).
+    assert _plan(64, 24, 4, 256, 16, 2048, 0)[2] == 256
+
+
 @pytest.mark.parametrize("args,code", [
     ((4, 24, 4, 256, 8, 100, 2048), _lib.TI_EUNSUPPORTED),    # page size not a multiple of 16
     ((4, 64, 2, 256, 16, 100, 2048), _lib.TI_EUNSUPPORTED),   # group of 32 > 16-row tile
@@ -190,8 +207,8 @@ def test_noalloc_decode_rejects_plans_beyond_its_scratch():
     lib = _lib.load()
     cap = lib.ti_gqa_decode_scratch_bytes()
     assert cap == 32 << 20
-    # 128 query heads over 8 KV heads: 128 balanced workgroups x 2 slots x 128 heads x (256 + 2)
-    # fp32 = 33.8 MB > 32 MiB.
+    # 128 query heads over 8 KV heads at 64 x 32k: 256 balanced runs (two whole rounds of 128)
+    # x 2 slots x 128 heads x (256 + 2) fp32 = 67.6 MB > 32 MiB.
     s, m, w = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
     _lib.check(lib.ti_gqa_decode_plan(64, 128, 8, 256, 16, 2048, 0, ctypes.byref(s),
                                       ctypes.byref(m), ctypes.byref(w)))

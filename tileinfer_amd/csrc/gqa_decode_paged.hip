@@ -687,16 +687,18 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
   out->balanced_wgs = 0;
   out->ws_balanced = 0;
   if (split_req <= 0) {
-    // Balanced mode: one round of workgroups over the batch's tiles; enough workgroups that no
-    // run exceeds the block ids one workgroup stages in LDS (a run may start mid-page: one page
-    // of slack).
+    // Balanced mode: one round of workgroups over the batch's tiles, one wave (KV head) per SIMD:
+    // cus * 4 / hkv runs per KV-head group, each a workgroup of the group's waves. (A second
+    // resident wave per SIMD, which head_dim 128 has room for, measured ~2 % slower at 8k-16k
+    // contexts: shorter runs pay more start-ups.) When runs that long would exceed the block ids
+    // one workgroup stages in LDS (a run may start mid-page: one page of slack), whole further
+    // rounds: a partial last round would run alone after the others and nearly double the time.
     const int64_t max_chunk = int64_t(kMaxSplitPages - 1) * (page_size / 16);
     const int64_t bound_tiles = ceil_div(bound, 16);
-    const int64_t wpb = (hkv % 4 == 0) ? 4 : (hkv % 2 == 0) ? 2 : 1;
-    const int64_t per_round = cus / (hkv / wpb) > 0 ? cus / (hkv / wpb) : 1;
+    const int64_t per_round = cus * 4 / hkv > 0 ? cus * 4 / hkv : 1;
+    const int64_t needed = ceil_div(int64_t(batch) * bound_tiles, max_chunk);
     int64_t wgs = per_round;
-    wgs = wgs > ceil_div(int64_t(batch) * bound_tiles, max_chunk)
-              ? wgs : ceil_div(int64_t(batch) * bound_tiles, max_chunk);
+    if (needed > wgs) wgs = ceil_div(needed, per_round) * per_round;
     if (wgs > 65535) return fail(TI_EINVAL, "decode: %lld balanced workgroups", (long long)wgs);
     out->balanced_wgs = int32_t(wgs);
     out->chunk_min_tiles = int32_t(kMinChunkTiles < max_chunk ? kMinChunkTiles : max_chunk);
