@@ -109,6 +109,11 @@ struct DecodeArgs {
   uint16_t* out;   // [B, hq, D]
   float* part_o;   // [B, hq, max_splits, D]
   float* part_ml;  // [B, hq, max_splits, 2]  (running max in log2 units, sum of exp2)
+  // Balanced mode: [B + 1] ints after the partials; entry b is sequence b's first tile in the
+  // batch's concatenated tile order (written by the workgroup that holds that tile, for sequences
+  // with tiles), entry B the batch's total tiles (written by workgroup 0). The merge reads them
+  // instead of scanning every sequence length per row.
+  int32_t* seq_first_tile;
   int32_t num_blocks32;  // block ids in [0, num_blocks32) are valid (int32 ids)
   int32_t hq, hkv, group, page_size, max_blocks, max_splits, split_tokens;
   float scale_log2;

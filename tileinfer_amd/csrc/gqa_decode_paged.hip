@@ -65,12 +65,6 @@ __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
   return x;
 }
 
-__device__ __forceinline__ int wave_sum(int x) {
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) x += __shfl_xor(x, d, 64);
-  return x;
-}
-
 // Total 16-token tiles of the batch and the balanced run length (same in every workgroup and in
 // the merge: a pure function of the sequence lengths and the plan).
 __device__ __forceinline__ int balanced_chunk(const DecodeArgs& a, int total_tiles) {
@@ -343,31 +337,46 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
   // 16-token tiles. Wave 0 finds the first and last sequence of that run with a prefix scan.
   const int i = blockIdx.y;
   if (wave == 0) {
-    int tot = 0;
-    for (int b0 = 0; b0 < batch; b0 += 64) {
-      tot += wave_sum(b0 + lane < batch ? seq_tiles(a, b0 + lane) : 0);
-    }
+    // Lane l owns sequences [l K, l K + K), K = ceil(batch / 64): it sums their tile counts (the
+    // loads issued together, so any batch costs about one memory latency), the lane sums are
+    // prefix-scanned, and the lanes whose blocks hold the run's first tile T0 and last tile
+    // T1 - 1 walk their own sequences to find them.
+    const int K = (batch + 63) >> 6;
+    const int j0 = min(lane * K, batch);
+    const int j1 = min(j0 + K, batch);
+    int mine = 0;
+#pragma unroll 8
+    for (int j = j0; j < j1; ++j) mine += seq_tiles(a, j);
+    const int incl = wave_inclusive_scan(mine, lane);
+    const int excl = incl - mine;
+    const int tot = __shfl(incl, 63, 64);
+    if (i == 0 && blockIdx.x == 0 && lane == 0 && a.seq_first_tile) a.seq_first_tile[batch] = tot;
     const int chunk = balanced_chunk(a, tot);
     const int T0 = i * chunk;
     const int T1 = min(T0 + chunk, tot);
-    int carry = 0, b_first = -1, s_first = 0, b_last = -1;
+    int b_first = -1, s_first = 0, b_last = -1;
     if (T0 < T1) {
-      for (int b0 = 0; b0 < batch && carry < T1; b0 += 64) {
-        const int nt = b0 + lane < batch ? seq_tiles(a, b0 + lane) : 0;
-        const int incl = wave_inclusive_scan(nt, lane) + carry;
-        const int excl = incl - nt;
-        const bool has_first = nt > 0 && excl <= T0 && T0 < incl;
-        const bool has_last = nt > 0 && excl <= T1 - 1 && T1 - 1 < incl;
-        const uint64_t mf = __builtin_amdgcn_ballot_w64(has_first);
-        const uint64_t ml = __builtin_amdgcn_ballot_w64(has_last);
-        if (mf) {
-          const int src = __builtin_ctzll(mf);
-          b_first = b0 + src;
-          s_first = __shfl(excl, src, 64);
+      const bool own_first = mine > 0 && excl <= T0 && T0 < incl;
+      const bool own_last = mine > 0 && excl <= T1 - 1 && T1 - 1 < incl;
+      int bf = -1, sf = 0, bl = -1;
+      if (own_first || own_last) {
+        int s = excl;
+        for (int j = j0; j < j1; ++j) {
+          const int nt = seq_tiles(a, j);
+          if (own_first && nt > 0 && s <= T0 && T0 < s + nt) {
+            bf = j;
+            sf = s;
+          }
+          if (own_last && nt > 0 && s <= T1 - 1 && T1 - 1 < s + nt) bl = j;
+          s += nt;
         }
-        if (ml) b_last = b0 + __builtin_ctzll(ml);
-        carry = __shfl(incl, 63, 64);
       }
+      // Each of the two tiles lies in exactly one lane's block.
+      const int lf = __builtin_ctzll(__builtin_amdgcn_ballot_w64(own_first));
+      const int ll = __builtin_ctzll(__builtin_amdgcn_ballot_w64(own_last));
+      b_first = __shfl(bf, lf, 64);
+      s_first = __shfl(sf, lf, 64);
+      b_last = __shfl(bl, ll, 64);
     }
     if (lane == 0) {
       s_part[0] = T0;
@@ -389,6 +398,10 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     if (nb > 0) {
       const int t0 = max(T0, sb) - sb;
       const int t1 = min(T1, sb + nb) - sb;
+      // The workgroup holding the sequence's first tile records where it starts for the merge.
+      if (t0 == 0 && blockIdx.x == 0 && threadIdx.x == 0 && a.seq_first_tile) {
+        a.seq_first_tile[b] = sb;
+      }
       const int ctx = __builtin_amdgcn_readfirstlane(seq_len(a, b));
       run_partition(b, 16 * t0, min(16 * t1, ctx));
       if (head_ok) {
@@ -404,13 +417,17 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
 // workgroup, in workgroup order (deterministic): m = max m_s, w_s = 2^(m_s - m),
 // out = sum w_s o_s / sum w_s l_s. In balanced mode it also writes the zero rows of empty
 // sequences (no workgroup covers them).
-template <int D, typename Tag>
-__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batch) {
+// W > 1 (small balanced batches): W waves per row; a row cut into more than 64 parts has them
+// split into W contiguous quarters, each summed in order by one wave, the quarters then added in
+// wave order (deterministic; a row of 64 parts or fewer takes the one-wave path unchanged).
+template <int D, typename Tag, int W>
+__global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int batch) {
   constexpr int PER = D / 64;  // d-values per thread
   typedef float PartVec __attribute__((ext_vector_type(PER)));  // one lane's piece of a part row
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = W > 1 ? __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6) : 0;
   const int d0 = lane * PER;
   uint16_t* orow = a.out + (int64_t(b) * a.hq + h) * D + d0;
   const uint16_t* grow = a.gate ? a.gate + b * a.gate_sb + int64_t(h) * a.gate_sh + d0 : nullptr;
@@ -452,6 +469,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
     slot0 = (int64_t(b) * a.hq + h) * a.max_splits;
   } else {
     const int nb = seq_tiles(a, b);
+    if (nb == 0 && wave != 0) return;  // uniform: one wave writes what follows
     if (nb == 0 && h == 0 && a.app_slot != nullptr) {
       // Fused append of a sequence no partial workgroup covers: its whole K/V row, here.
       const int slot = a.app_slot[b];
@@ -477,15 +495,10 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
       for (int j = 0; j < PER; j += 2) put(j, pack2(e[j] * inv, e[j + 1] * inv, Tag{}));
       return;
     }
-    int tot = 0, pre_tiles = 0;
-    for (int b0 = 0; b0 < batch; b0 += 64) {
-      const int j = b0 + lane;
-      const int nt = j < batch ? seq_tiles(a, j) : 0;
-      tot += nt;
-      pre_tiles += j < b ? nt : 0;
-    }
-    tot = wave_sum(tot);
-    pre_tiles = wave_sum(pre_tiles);
+    // Where the sequence's tiles start in the batch's tile order, and the batch's total, as the
+    // partial kernel recorded them.
+    const int pre_tiles = __builtin_amdgcn_readfirstlane(a.seq_first_tile[b]);
+    const int tot = __builtin_amdgcn_readfirstlane(a.seq_first_tile[batch]);
     const int chunk = balanced_chunk(a, tot);
     const int i0 = pre_tiles / chunk;
     const int i1 = (pre_tiles + nb - 1) / chunk;
@@ -499,6 +512,76 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
   auto part = [&](int s) -> int64_t {
     return slot0 + s * stride + ((s == 0 && first_part_slot1) ? a.hq : 0);
   };
+  if constexpr (W > 1) {
+    if (nparts <= 64) {  // uniform
+      if (wave != 0) return;
+    } else {
+      __shared__ float s_red[W - 1][PER + 1][64];  // the other waves' sums (o, then l)
+      float m = -INFINITY;
+#pragma unroll 4
+      for (int s0 = 0; s0 < nparts; s0 += 64) {
+        const int s = s0 + lane;
+        m = fmaxf(m, s < nparts ? a.part_ml[2 * part(s)] : -INFINITY);
+      }
+#pragma unroll
+      for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+      m = fmaxf(m, me);
+      float acc[PER];
+#pragma unroll
+      for (int j = 0; j < PER; ++j) acc[j] = 0.f;
+      float l = 0.f;
+      if (wave == 0 && me != -INFINITY) l = add_pre(m, acc);  // the prefix parts first
+      if (m != -INFINITY) {
+        const int quarter = (nparts + W - 1) / W;
+        const int p0 = min(wave * quarter, nparts);
+        const int p1 = min(p0 + quarter, nparts);
+        for (int s0 = p0; s0 < p1; s0 += 64) {
+          const int s = s0 + lane;
+          float w = 0.f, wl = 0.f;
+          if (s < p1) {
+            const float ms = a.part_ml[2 * part(s)];
+            w = ms == -INFINITY ? 0.f : fast_exp2(ms - m);
+            wl = w * a.part_ml[2 * part(s) + 1];
+          }
+          const int cnt = __builtin_amdgcn_readfirstlane(min(64, p1 - s0));
+          for (int j0 = 0; j0 < cnt; j0 += 16) {
+            PartVec v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+              const int j = min(j0 + u, cnt - 1);
+              v[u] = *reinterpret_cast<const PartVec*>(a.part_o + part(s0 + j) * D + d0);
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+              if (j0 + u < cnt) {  // uniform
+                const float wj = __shfl(w, j0 + u, 64);
+                const float lj = __shfl(wl, j0 + u, 64);
+#pragma unroll
+                for (int q = 0; q < PER; ++q) acc[q] += wj * v[u][q];
+                l += lj;
+              }
+            }
+          }
+        }
+      }
+      if (wave > 0) {
+#pragma unroll
+        for (int q = 0; q < PER; ++q) s_red[wave - 1][q][lane] = acc[q];
+        s_red[wave - 1][PER][lane] = l;
+      }
+      __syncthreads();
+      if (wave != 0) return;
+      for (int w = 0; w < W - 1; ++w) {
+#pragma unroll
+        for (int q = 0; q < PER; ++q) acc[q] += s_red[w][q][lane];
+        l += s_red[w][PER][lane];
+      }
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+      for (int j = 0; j < PER; j += 2) put(j, pack2(acc[j] * inv, acc[j + 1] * inv, Tag{}));
+      return;
+    }
+  }
   // The o rows of the first kBurst parts are requested ahead of the (m, l) loads: they do not
   // depend on the weights, so one memory latency covers both. Past nparts the last part's row is
   // read again (a valid row) and left out of the sum. nburst is uniform; readfirstlane lets the
@@ -513,7 +596,8 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
   // Maximum over the parts' m (and the prefix parts'), lane-parallel; lane s keeps the (m, l) of
   // part s (parts 0-63) for the weights below.
   float m = -INFINITY, ms0 = -INFINITY, ls0 = 0.f;
-  for (int s0 = 0; s0 < nparts; s0 += 64) {
+#pragma unroll 4
+  for (int s0 = 0; s0 < nparts; s0 += 64) {  // unrolled: the loads of 4 steps issued together
     const int s = s0 + lane;
     float ms = -INFINITY;
     if (s < nparts) {
@@ -534,16 +618,13 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
   if (m != -INFINITY) {
     // Parts in chunks of 64: lane s holds part s0+s's weight w and w * l; part j's are broadcast
     // when it is added. Summation order is fixed (ascending part) for o and for l.
+    float ms = ms0, ls = ls0;  // (m, l) of part s0 + lane of the current chunk
     for (int s0 = 0; s0 < nparts; s0 += 64) {
-      const int s = s0 + lane;
-      float ms = ms0, ls = ls0;
-      if (s0 > 0) {
-        ms = -INFINITY;
-        ls = 0.f;
-        if (s < nparts) {
-          ms = a.part_ml[2 * part(s)];
-          ls = a.part_ml[2 * part(s) + 1];
-        }
+      // The next chunk's (m, l) are requested now, ahead of this chunk's o rows.
+      float ms_next = -INFINITY, ls_next = 0.f;
+      if (s0 + 64 + lane < nparts) {
+        ms_next = a.part_ml[2 * part(s0 + 64 + lane)];
+        ls_next = a.part_ml[2 * part(s0 + 64 + lane) + 1];
       }
       const float w = ms == -INFINITY ? 0.f : fast_exp2(ms - m);
       const float wl = w * ls;
@@ -563,19 +644,21 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int batc
         }
         j0 = kBurst;
       }
-      // The rest 8 at a time, loaded back to back so that their latencies overlap.
-      for (; j0 < cnt; j0 += 8) {
-        PartVec v[8];
+      // The rest 16 at a time, loaded back to back so that their latencies overlap.
+      for (; j0 < cnt; j0 += 16) {
+        PartVec v[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < 16; ++u) {
           const int j = min(j0 + u, cnt - 1);
           v[u] = *reinterpret_cast<const PartVec*>(a.part_o + part(s0 + j) * D + d0);
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < 16; ++u) {
           if (j0 + u < cnt) add_part(j0 + u, v[u]);  // uniform
         }
       }
+      ms = ms_next;
+      ls = ls_next;
     }
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -597,6 +680,11 @@ int launch_mfma(const DecodeArgs& a, int batch, bool reuse_kv, hipStream_t strea
   return check_launch("ti_gqa_decode_paged (mfma)");
 }
 
+// Balanced calls of at most this many sequences merge with 4 waves per row: only a few
+// sequences can each be cut into more than 64 parts, and the merge of such a row is a chain of
+// dependent loads that 4 waves shorten 4-fold (B = 1 at 128k: 256 parts per row).
+constexpr int kWideMergeBatch = 4;
+
 template <int D, typename Tag>
 int launch_decode(const DecodeArgs& a, int batch, bool reuse_kv, hipStream_t stream) {
   int rc;
@@ -608,8 +696,13 @@ int launch_decode(const DecodeArgs& a, int batch, bool reuse_kv, hipStream_t str
     rc = launch_mfma<D, Tag, 1>(a, batch, reuse_kv, stream);
   }
   if (rc != TI_OK) return rc;
+  if (a.balanced_wgs > 0 && batch <= kWideMergeBatch) {
+    hipLaunchKernelGGL((decode_merge_kernel<D, Tag, 4>), dim3(a.hq, batch), dim3(256), 0, stream,
+                       a, batch);
+    return check_launch("ti_gqa_decode_paged (merge)");
+  }
   if (a.balanced_wgs > 0 || a.max_splits > 1) {
-    hipLaunchKernelGGL((decode_merge_kernel<D, Tag>), dim3(a.hq, batch), dim3(64), 0, stream, a,
+    hipLaunchKernelGGL((decode_merge_kernel<D, Tag, 1>), dim3(a.hq, batch), dim3(64), 0, stream, a,
                        batch);
     return check_launch("ti_gqa_decode_paged (merge)");
   }
@@ -702,7 +795,8 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
     if (wgs > 65535) return fail(TI_EINVAL, "decode: %lld balanced workgroups", (long long)wgs);
     out->balanced_wgs = int32_t(wgs);
     out->chunk_min_tiles = int32_t(kMinChunkTiles < max_chunk ? kMinChunkTiles : max_chunk);
-    out->ws_balanced = wgs * 2 * hq * (D + 2) * 4;
+    // Partials, then the [batch + 1] first-tile entries (rounded to 256 bytes).
+    out->ws_balanced = wgs * 2 * hq * (D + 2) * 4 + (int64_t(batch) * 4 + 4 + 255) / 256 * 256;
   }
   return TI_OK;
 }
@@ -799,6 +893,8 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
   const int64_t n_parts =
       balanced ? int64_t(pl.balanced_wgs) * 2 * num_q_heads : int64_t(batch) * num_q_heads * max_splits;
   a.part_ml = a.part_o ? a.part_o + n_parts * head_dim : nullptr;
+  a.seq_first_tile =
+      balanced && a.part_o ? reinterpret_cast<int32_t*>(a.part_ml + n_parts * 2) : nullptr;
   a.balanced_wgs = balanced ? pl.balanced_wgs : 0;
   a.chunk_min_tiles = pl.chunk_min_tiles;
   a.num_blocks32 = int32_t(num_blocks < INT32_MAX ? num_blocks : INT32_MAX);
@@ -859,11 +955,11 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
     if (rc != TI_OK) return rc;
     if (max_splits > 1) {
       if (head_dim == 256) {
-        if (bf16) hipLaunchKernelGGL((decode_merge_kernel<256, Bf16>), dim3(num_q_heads, batch), dim3(64), 0, s, a, batch);
-        else hipLaunchKernelGGL((decode_merge_kernel<256, F16>), dim3(num_q_heads, batch), dim3(64), 0, s, a, batch);
+        if (bf16) hipLaunchKernelGGL((decode_merge_kernel<256, Bf16, 1>), dim3(num_q_heads, batch), dim3(64), 0, s, a, batch);
+        else hipLaunchKernelGGL((decode_merge_kernel<256, F16, 1>), dim3(num_q_heads, batch), dim3(64), 0, s, a, batch);
       } else {
-        if (bf16) hipLaunchKernelGGL((decode_merge_kernel<128, Bf16>), dim3(num_q_heads, batch), dim3(64), 0, s, a, batch);
-        else hipLaunchKernelGGL((decode_merge_kernel<128, F16>), dim3(num_q_heads, batch), dim3(64), 0, s, a, batch);
+        if (bf16) hipLaunchKernelGGL((decode_merge_kernel<128, Bf16, 1>), dim3(num_q_heads, batch), dim3(64), 0, s, a, batch);
+        else hipLaunchKernelGGL((decode_merge_kernel<128, F16, 1>), dim3(num_q_heads, batch), dim3(64), 0, s, a, batch);
       }
       return check_launch("ti_gqa_decode_paged (merge)");
     }
