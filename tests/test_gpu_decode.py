@@ -205,6 +205,32 @@ def test_long_context_32k(dev):
     assert_decode_close(out, ref)
 
 
+def test_one_long_sequence_many_parts(dev):
+    """One 100,003-token sequence: the balanced plan cuts it into one part per workgroup (far more
+    than 64), which the merge sums as four ordered quarters, the ragged tail tile included."""
+    say("decode 1 x 100003")
+    step = make_step([100003], pool=6300, seed=1010)
+    out, _, _ = gpu_step(step, dev)
+    ref, _, _ = cpu_step(step)
+    assert_decode_close(out, ref)
+
+
+def test_many_short_sequences(dev):
+    """1,500 sequences of 0 to 300 tokens: each workgroup's run crosses many sequences; the merge
+    finds each cut sequence's parts from the first-tile entries the partial kernel records, and
+    writes the zero rows of the empty ones."""
+    g = torch.Generator().manual_seed(1011)
+    ctx = torch.randint(0, 301, (1500,), generator=g)
+    ctx[::97] = 0
+    ctx = ctx.tolist()
+    say(f"decode 1500 short sequences, {sum(ctx)} tokens")
+    step = make_step(ctx, pool=sum((c + 15) // 16 for c in ctx) + 16, seed=1011)
+    out, _, _ = gpu_step(step, dev)
+    ref, _, _ = cpu_step(step)
+    assert_decode_close(out, ref)
+    assert not bool(out[::97].float().abs().sum())
+
+
 def test_graph_capture_replay(dev):
     """Append + decode captured in a HIP graph; every replay matches the eager result."""
     say("graph capture")
