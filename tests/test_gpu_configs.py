@@ -170,7 +170,7 @@ def test_runner_padding_rows(prefixed, dev):
     flat(ek)[live] = kn[:n].reshape(n, -1)
     flat(ev)[live] = vn[:n].reshape(n, -1)
     assert torch.equal(bits(kv), bits(expect)), "a padding row wrote into the cache"
-    kw = {"shared_prefix_tokens": p, "kv_reuse": True} if prefixed else {}
+    kw = {"shared_prefix_tokens": p, "prefix_pass": "always", "kv_reuse": True} if prefixed else {}
     out = gqa_decode_paged_fn(q, k_paged, v_paged, tables, ctx, BLOCK, **kw)
     assert bool((out[n:] == 0).all()), "padding rows must decode to zeros"
     unpadded = gqa_decode_paged_fn(q[:n].contiguous(), k_paged, v_paged, tables[:n], ctx[:n],

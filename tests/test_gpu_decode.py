@@ -371,14 +371,14 @@ def test_shared_prefix_decode(suffix, prefix, split, dev):
     d_q, d_kc, d_vc, d_seq = q.to(dev), kc.to(dev), vc.to(dev), seq.to(dev)
     run = lambda tbl, **kw: gqa_decode_paged_fn(d_q, d_kc, d_vc, tbl.to(dev), d_seq,  # noqa: E731
                                                 split_tokens=split, **kw)
-    out_shared = run(shared, shared_prefix_tokens=prefix, kv_reuse=True)
-    out_private = run(private, shared_prefix_tokens=prefix)
+    out_shared = run(shared, shared_prefix_tokens=prefix, prefix_pass="always", kv_reuse=True)
+    out_private = run(private, shared_prefix_tokens=prefix, prefix_pass="always")
     assert_decode_close(out_shared, ref)
     assert_decode_close(out_shared, run(shared))
     assert torch.equal(bits(out_shared), bits(out_private))
     gate = (2 * torch.randn(len(suffix), 1, 24 * 256, generator=torch.Generator().manual_seed(9))
             ).to(torch.bfloat16).to(dev)
-    gated = run(shared, shared_prefix_tokens=prefix, gate=gate)
+    gated = run(shared, shared_prefix_tokens=prefix, prefix_pass="always", gate=gate)
     from tileinfer_amd.kernels import fused_sigmoid_mul
     assert torch.equal(bits(gated), bits(fused_sigmoid_mul(out_shared, gate.view_as(out_shared))))
 
@@ -391,8 +391,12 @@ def test_shared_prefix_zero_and_whole_context(dev):
     args = (q.to(dev), kc.to(dev), vc.to(dev), shared.to(dev), seq.to(dev))
     plain = gqa_decode_paged_fn(*args)
     assert torch.equal(bits(gqa_decode_paged_fn(*args, shared_prefix_tokens=0)), bits(plain))
-    assert_decode_close(gqa_decode_paged_fn(*args, shared_prefix_tokens=640),
+    # Three sequences are below the prefix pass's break-even: "auto" is the plain call, bitwise.
+    assert torch.equal(bits(gqa_decode_paged_fn(*args, shared_prefix_tokens=640)), bits(plain))
+    assert_decode_close(gqa_decode_paged_fn(*args, shared_prefix_tokens=640, prefix_pass="always"),
                         ref_gqa_decode_paged(q, kc, vc, shared, seq))
+    with pytest.raises(ValueError):
+        gqa_decode_paged_fn(*args, shared_prefix_tokens=640, prefix_pass="never")
     with pytest.raises(ValueError):
         gqa_decode_paged_fn(*args, shared_prefix_tokens=100)        # not a page multiple
     with pytest.raises(ValueError):
@@ -408,7 +412,8 @@ def test_shared_prefix_graph_capture_replay(dev):
     args = (kc.to(dev), vc.to(dev), shared.to(dev), seq.to(dev))
 
     def fn():
-        return gqa_decode_paged_fn(q, *args, kv_reuse=True, shared_prefix_tokens=1024)
+        return gqa_decode_paged_fn(q, *args, kv_reuse=True, shared_prefix_tokens=1024,
+                                   prefix_pass="always")
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())

@@ -101,7 +101,7 @@ def test_shared_prefix_decode_high_pages(pool, dev):
     q = torch.randn(len(own), HQ, D, generator=g).to(torch.bfloat16)
     seqlen = torch.tensor([prefix + n for n in own], dtype=torch.int32)
     args = (q.to(dev), pool[0], pool[1], pool_t.to(dev), seqlen.to(dev), BS)
-    shared = gqa_decode_paged_fn(*args, shared_prefix_tokens=prefix)
+    shared = gqa_decode_paged_fn(*args, shared_prefix_tokens=prefix, prefix_pass="always")
     plain = gqa_decode_paged_fn(*args)
     ref = ref_gqa_decode_paged(q, kc, vc, compact_t, seqlen, BS)
     assert_decode_close(shared, ref)

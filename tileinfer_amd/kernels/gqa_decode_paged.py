@@ -44,6 +44,12 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
     return s.value, m.value, w.value
 
 
+# Where attending a shared prefix once (prefill pass over the prefix, suffix decode, merge) beats
+# the plain decode reading the prefix pages per sequence (cache-keeping policy: they hit in
+# L2/MALL): the pass has a fixed cost of ~30-75 us, so it needs enough sequences and prefix.
+_PREFIX_MIN_BATCH, _PREFIX_MIN_TOKENS = 8, 131072
+
+
 @functools.lru_cache(maxsize=256)
 def _prefix_splits(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
                    prefix_tokens: int) -> int:
@@ -159,6 +165,7 @@ def gqa_decode_paged_fn(
     kv_reuse: bool = False,
     gate: torch.Tensor | None = None,
     shared_prefix_tokens: int = 0,
+    prefix_pass: str = "auto",
     append: tuple | None = None,
 ) -> torch.Tensor:
     """Single-query paged GQA attention.
@@ -188,6 +195,12 @@ def gqa_decode_paged_fn(
             tokens [P, seqlen) of each sequence and merges the two parts. Within the decode
             tolerance of the plain call; bitwise the same for shared and private prefix pages.
             MFMA variant only.
+        prefix_pass: keyword-only, with ``shared_prefix_tokens``: "auto" attends the prefix once
+            only where that is faster than the plain decode, i.e. for at least 8 sequences and
+            B x P >= 131,072 prefix tokens (measured against the plain call with the
+            cache-keeping policy: the prefix pass wins from 16 sequences at an 8k prefix, from 64
+            at 2k and from 8 at 32k); below that the call is the plain decode, bitwise. "always"
+            takes the prefix pass for any batch.
         append: keyword-only ``(key, value, slot_mapping)``, the decode step's new token per
             sequence (key/value [B, H_kv, D] in q's dtype, slot_mapping [B] int32 with
             slot_mapping[b] the slot of position seqlen_kv[b] - 1, or -1 to skip): written into
@@ -219,6 +232,10 @@ def gqa_decode_paged_fn(
                              f"{page_size} within the block table's {width} pages")
         if variant == "scalar":
             raise ValueError("shared_prefix_tokens needs the MFMA variant")
+        if prefix_pass not in ("auto", "always"):
+            raise ValueError(f"prefix_pass must be 'auto' or 'always', got {prefix_pass!r}")
+        if prefix_pass == "auto" and (b < _PREFIX_MIN_BATCH or b * prefix < _PREFIX_MIN_TOKENS):
+            prefix = 0  # the plain decode is the faster one here
         # The batch's queries as the B "tokens" of one non-causal chunk over sequence 0's prefix,
         # its keys cut into `splits` ranges, each range's unnormalised part merged by the decode.
         splits = _prefix_splits(b, h_q, h_kv, d, prefix)
