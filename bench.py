@@ -494,6 +494,7 @@ def metric_extras(kv, tables, seqlen, q, dev, args) -> dict:
         ctx *= 2
     res["decode_ctx_sweep_batch64"] = sweep
     res["other_configs"] = other_configs_decode(dev, args)
+    res["decode_other_shapes"] = decode_shapes_extras(dev, args)
     res["prefill_config4"] = prefill_extras(dev, args)
     return res
 
@@ -599,6 +600,29 @@ def other_configs_decode(dev, args) -> dict:
                              "L2/MALL, so the logical % can exceed 100); shared_prefix: the "
                              "8,192-token prefix attended once for the batch")
         res[f"config{cfg}"] = entry
+        del st
+    return res
+
+
+def decode_shapes_extras(dev, args) -> dict:
+    """The decode at head shapes and batch layouts besides the BASELINE configs (random tables,
+    N(0,1) values, HIP events): the reference's own self-test shape at its default batch
+    (kernels/gqa_decode_paged.py:472-512: B 32, 32 query / 8 KV heads, head_dim 128, 8k), head_dim
+    128 at 64 x 32k, one 128k-token sequence, and 1,024 sequences of 512 tokens."""
+    from tileinfer_amd import workloads as wl
+
+    res = {}
+    for name, b, ctx, hq, hkv, d in (("ref_selftest_b32_hq32_hkv8_d128_8k", 32, 8192, 32, 8, 128),
+                                     ("b64_hq32_hkv8_d128_32k", 64, 32768, 32, 8, 128),
+                                     ("b1_128k", 1, 131072, HQ, HKV, HEAD_DIM),
+                                     ("b1024_512", 1024, 512, HQ, HKV, HEAD_DIM)):
+        st = wl.make_step([ctx] * b, pool=b * ctx // BLOCK, seed=31, device=dev, hq=hq, hkv=hkv,
+                          d=d)
+        nbytes = decode_bytes([ctx] * b, hq=hq, hkv=hkv, d=d)
+        us = _time(lambda: gqa_decode_paged_fn(st.q, st.k_cache, st.v_cache, st.block_table,
+                                               st.seqlen, BLOCK), args.steps, args.warmup)
+        res[name] = {"us": round(us, 2), "GBps_algorithmic": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "pct_of_peak_hbm": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 2)}
         del st
     return res
 
