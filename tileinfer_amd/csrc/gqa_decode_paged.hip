@@ -339,8 +339,8 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
   if (wave == 0) {
     // Lane l owns sequences [l K, l K + K), K = ceil(batch / 64): it sums their tile counts (the
     // loads issued together, so any batch costs about one memory latency), the lane sums are
-    // prefix-scanned, and the lanes whose blocks hold the run's first tile T0 and last tile
-    // T1 - 1 walk their own sequences to find them.
+    // prefix-scanned, and the blocks holding the run's first tile T0 and last tile T1 - 1 are
+    // searched.
     const int K = (batch + 63) >> 6;
     const int j0 = min(lane * K, batch);
     const int j1 = min(j0 + K, batch);
@@ -356,27 +356,35 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     const int T1 = min(T0 + chunk, tot);
     int b_first = -1, s_first = 0, b_last = -1;
     if (T0 < T1) {
-      const bool own_first = mine > 0 && excl <= T0 && T0 < incl;
-      const bool own_last = mine > 0 && excl <= T1 - 1 && T1 - 1 < incl;
-      int bf = -1, sf = 0, bl = -1;
-      if (own_first || own_last) {
-        int s = excl;
-        for (int j = j0; j < j1; ++j) {
-          const int nt = seq_tiles(a, j);
-          if (own_first && nt > 0 && s <= T0 && T0 < s + nt) {
-            bf = j;
-            sf = s;
+      // Each of the two tiles lies in exactly one lane's block; the whole wave then scans that
+      // block 64 sequences at a time (one memory latency per 64 of its K sequences).
+      const int lf = __builtin_ctzll(
+          __builtin_amdgcn_ballot_w64(mine > 0 && excl <= T0 && T0 < incl));
+      const int ll = __builtin_ctzll(
+          __builtin_amdgcn_ballot_w64(mine > 0 && excl <= T1 - 1 && T1 - 1 < incl));
+      // The sequence holding tile t of lane `owner`'s block and the first tile of that sequence.
+      auto locate = [&](int owner, int t, int& b_at, int& s_at) {
+        const int jb = min(owner * K, batch);
+        const int je = min(jb + K, batch);
+        int base = __shfl(excl, owner, 64);
+        for (int c0 = jb; c0 < je; c0 += 64) {
+          const int j = c0 + lane;
+          const int nt = j < je ? seq_tiles(a, j) : 0;
+          const int inc = wave_inclusive_scan(nt, lane) + base;
+          const int exc = inc - nt;
+          const uint64_t hit = __builtin_amdgcn_ballot_w64(nt > 0 && exc <= t && t < inc);
+          if (hit) {  // uniform
+            const int src = __builtin_ctzll(hit);
+            b_at = c0 + src;
+            s_at = __shfl(exc, src, 64);
+            return;
           }
-          if (own_last && nt > 0 && s <= T1 - 1 && T1 - 1 < s + nt) bl = j;
-          s += nt;
+          base = __shfl(inc, 63, 64);
         }
-      }
-      // Each of the two tiles lies in exactly one lane's block.
-      const int lf = __builtin_ctzll(__builtin_amdgcn_ballot_w64(own_first));
-      const int ll = __builtin_ctzll(__builtin_amdgcn_ballot_w64(own_last));
-      b_first = __shfl(bf, lf, 64);
-      s_first = __shfl(sf, lf, 64);
-      b_last = __shfl(bl, ll, 64);
+      };
+      int s_last = 0;
+      locate(lf, T0, b_first, s_first);
+      locate(ll, T1 - 1, b_last, s_last);
     }
     if (lane == 0) {
       s_part[0] = T0;
