@@ -236,6 +236,7 @@ def gqa_decode_paged_fn(
             raise ValueError(f"prefix_pass must be 'auto' or 'always', got {prefix_pass!r}")
         if prefix_pass == "auto" and (b < _PREFIX_MIN_BATCH or b * prefix < _PREFIX_MIN_TOKENS):
             prefix = 0  # the plain decode is the faster one here
+    if prefix:
         # The batch's queries as the B "tokens" of one non-causal chunk over sequence 0's prefix,
         # its keys cut into `splits` ranges, each range's unnormalised part merged by the decode.
         splits = _prefix_splits(b, h_q, h_kv, d, prefix)
