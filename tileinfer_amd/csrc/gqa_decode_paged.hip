@@ -367,6 +367,11 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
         const int jb = min(owner * K, batch);
         const int je = min(jb + K, batch);
         int base = __shfl(excl, owner, 64);
+        if (K == 1) {  // uniform: the owner's block is its one sequence, already scanned
+          b_at = jb;
+          s_at = base;
+          return;
+        }
         for (int c0 = jb; c0 < je; c0 += 64) {
           const int j = c0 + lane;
           const int nt = j < je ? seq_tiles(a, j) : 0;
