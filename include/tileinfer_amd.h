@@ -366,7 +366,10 @@ int ti_gqa_decode_paged_append(const void* q, int64_t q_stride_b, int64_t q_stri
  * ti_gqa_prefill_paged_partial writes them with key_splits = prefix_parts), in part order. Rows
  * with seqlen[b] < prefix_tokens (graph padding) get no prefix part.
  * Same arguments as ti_gqa_decode_paged_gated otherwise (gate may be NULL); the workspace is
- * ti_gqa_decode_plan's for max_blocks_per_seq - prefix_tokens / page_size. MFMA variant only.
+ * ti_gqa_decode_plan's for max_blocks_per_seq - prefix_tokens / page_size, plus
+ * batch * num_q_heads * (head_dim + 2) * 4 bytes when split_tokens is 0 (the balanced plan keeps
+ * the rows of sequences one workgroup covers whole there, for the merge to fold the prefix parts
+ * into). MFMA variant only.
  * Reference counterpart: gqa_decode_paged_fn (kernels/gqa_decode_paged.py:392-437) on a batch
  * whose block tables share a prefix (engine/scheduler.py:161-189 share_blocks), which reads the
  * shared pages once per sequence.

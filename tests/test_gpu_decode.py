@@ -360,6 +360,7 @@ def _shared_prefix_step(suffix, prefix, seed, hq=24, hkv=4, d=256, page=16):
     ([0, 1, 700, 33, 4000, 16], 1024, None),     # empty and short suffixes, one cut over many runs
     ([300, 300, 5], 512, 256),                   # a fixed split
     ([90] * 40, 4096, None),                     # many sequences, long prefix
+    ([32] * 64, 1024, None),                     # every run covers two whole sequences
 ])
 def test_shared_prefix_decode(suffix, prefix, split, dev):
     """shared_prefix_tokens: the prefix attended once for the batch and merged into each row —

@@ -136,6 +136,11 @@ struct DecodeArgs {
   const float* pre_ml;
   int32_t pre_parts;
   int32_t ctx_offset;
+  // Balanced calls with prefix parts (whole_rows = 1): a sequence one workgroup covers whole
+  // stores its unnormalised row as part row whole_row0 + b * hq + h (after the workgroups' part
+  // rows), and the merge folds the prefix parts into it.
+  int32_t whole_rows;
+  int64_t whole_row0;
   // Optional fused append (one new token per sequence, its K/V rows not yet in the cache): row b
   // of app_k / app_v ([B][hkv * D] at row strides app_k_sb / app_v_sb elements) is written to
   // cache row app_slot[b] (skipped when negative or >= app_num_slots) before it is read, by the

@@ -418,8 +418,15 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
       const int ctx = __builtin_amdgcn_readfirstlane(seq_len(a, b));
       run_partition(b, 16 * t0, min(16 * t1, ctx));
       if (head_ok) {
-        if (t0 == 0 && t1 == nb) store_out(b);
-        else store_partial((int64_t(i) * 2 + (b == b_first ? 0 : 1)) * a.hq + h);
+        if (t0 == 0 && t1 == nb) {
+          // With precomputed prefix parts a whole sequence's row goes to its own part slot and
+          // the merge folds the prefix parts in (in parallel over rows, not one dependent load
+          // round per part in this epilogue).
+          if (a.whole_rows) store_partial(a.whole_row0 + int64_t(b) * a.hq + h);
+          else store_out(b);
+        } else {
+          store_partial((int64_t(i) * 2 + (b == b_first ? 0 : 1)) * a.hq + h);
+        }
       }
     }
     sb += nb;
@@ -455,20 +462,45 @@ __global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int 
   const int64_t part_rows = int64_t(batch) * a.hq;
   const bool pre = a.pre_o != nullptr && a.seqlen[b] >= a.ctx_offset;
   float me = -INFINITY;
-  if (pre) {
-    for (int s = 0; s < a.pre_parts; ++s) me = fmaxf(me, a.pre_ml[2 * (s * part_rows + pr)]);
+  if (pre) {  // uniform; lane s reads part s's maximum
+    for (int s0 = 0; s0 < a.pre_parts; s0 += 64) {
+      if (s0 + lane < a.pre_parts) me = fmaxf(me, a.pre_ml[2 * ((s0 + lane) * part_rows + pr)]);
+    }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) me = fmaxf(me, __shfl_xor(me, d, 64));
   }
-  // acc += sum_s 2^(m_s - m) o_s, returns sum_s 2^(m_s - m) l_s (parts in order). (Loading the
-  // parts lane-parallel, or all of them into registers first, measured no faster on config 5.)
+  // acc += sum_s 2^(m_s - m) o_s, returns sum_s 2^(m_s - m) l_s, summed in part order. Lane s
+  // computes part s's weights; the o rows are loaded 16 parts at a time before any is used, so
+  // their latencies overlap (one dependent load per part cost config 5's merge ~11 us).
   auto add_pre = [&](float m, float* acc) -> float {
     float l = 0.f;
-    for (int s = 0; s < a.pre_parts; ++s) {
-      const int64_t r = s * part_rows + pr;
-      const float ms = a.pre_ml[2 * r];
-      const float w = ms == -INFINITY ? 0.f : fast_exp2(ms - m);
+    for (int s0 = 0; s0 < a.pre_parts; s0 += 64) {
+      float w = 0.f, wl = 0.f;
+      if (s0 + lane < a.pre_parts) {
+        const int64_t r = (s0 + lane) * part_rows + pr;
+        const float ms = a.pre_ml[2 * r];
+        w = ms == -INFINITY ? 0.f : fast_exp2(ms - m);
+        wl = w * a.pre_ml[2 * r + 1];
+      }
+      const int cnt = __builtin_amdgcn_readfirstlane(min(64, a.pre_parts - s0));
+      for (int j0 = 0; j0 < cnt; j0 += 16) {
+        PartVec v[16];
 #pragma unroll
-      for (int q = 0; q < PER; ++q) acc[q] += w * a.pre_o[r * D + d0 + q];
-      l += w * a.pre_ml[2 * r + 1];
+        for (int u = 0; u < 16; ++u) {
+          const int j = min(j0 + u, cnt - 1);  // past cnt: a valid row, left out below
+          v[u] = *reinterpret_cast<const PartVec*>(a.pre_o + ((s0 + j) * part_rows + pr) * D + d0);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          if (j0 + u < cnt) {  // uniform
+            const float wj = __shfl(w, j0 + u, 64);
+            const float lj = __shfl(wl, j0 + u, 64);
+#pragma unroll
+            for (int q = 0; q < PER; ++q) acc[q] += wj * v[u][q];
+            l += lj;
+          }
+        }
+      }
     }
     return l;
   };
@@ -515,11 +547,16 @@ __global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int 
     const int chunk = balanced_chunk(a, tot);
     const int i0 = pre_tiles / chunk;
     const int i1 = (pre_tiles + nb - 1) / chunk;
-    if (i0 == i1) return;  // one workgroup covered the whole sequence and wrote it
-    nparts = i1 - i0 + 1;
-    first_part_slot1 = (i0 * chunk < pre_tiles) ? 1 : 0;
-    slot0 = int64_t(i0) * 2 * a.hq + h;
-    stride = 2 * a.hq;
+    if (i0 == i1) {  // one workgroup covered the whole sequence
+      if (!a.whole_rows) return;  // and wrote its row
+      nparts = 1;  // its row waits in the sequence's whole-row slot for the prefix parts
+      slot0 = a.whole_row0 + int64_t(b) * a.hq + h;
+    } else {
+      nparts = i1 - i0 + 1;
+      first_part_slot1 = (i0 * chunk < pre_tiles) ? 1 : 0;
+      slot0 = int64_t(i0) * 2 * a.hq + h;
+      stride = 2 * a.hq;
+    }
   }
   // Part s lives at slot0 + s * stride (+ hq for a first part stored as its workgroup's last).
   auto part = [&](int s) -> int64_t {
@@ -814,6 +851,10 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
   return TI_OK;
 }
 
+// Workspace bytes a balanced ti_gqa_decode_paged_prefixed call needs beyond the plan's: one part
+// row (o, then (m, l)) per (sequence, q-head) for the whole sequences.
+int64_t prefixed_extra_bytes(int64_t batch, int64_t hq, int64_t D) { return batch * hq * (D + 2) * 4; }
+
 }  // namespace
 }  // namespace ti
 
@@ -871,7 +912,11 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
   if (rc != TI_OK) return rc;
   const bool balanced = kind != TI_DECODE_SCALAR && pl.balanced_wgs > 0;
   const int32_t split = pl.split, max_splits = pl.max_splits;
-  const int64_t ws_need = balanced ? pl.ws_balanced : pl.ws_fixed;
+  // Balanced calls with prefix parts keep one more part row per (sequence, q-head): whole
+  // sequences leave their rows there for the merge.
+  const bool whole_rows = balanced && pre_o != nullptr;
+  const int64_t ws_need = (balanced ? pl.ws_balanced : pl.ws_fixed) +
+                          (whole_rows ? prefixed_extra_bytes(batch, num_q_heads, head_dim) : 0);
   if (batch == 0) return TI_OK;
   if (!q || !k_cache || !v_cache || !block_table || !seqlen || !out) {
     return fail(TI_EINVAL, "ti_gqa_decode_paged: null pointer");
@@ -904,7 +949,10 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
   a.out = static_cast<uint16_t*>(out);
   a.part_o = static_cast<float*>(workspace);
   const int64_t n_parts =
-      balanced ? int64_t(pl.balanced_wgs) * 2 * num_q_heads : int64_t(batch) * num_q_heads * max_splits;
+      (balanced ? int64_t(pl.balanced_wgs) * 2 * num_q_heads : int64_t(batch) * num_q_heads * max_splits) +
+      (whole_rows ? int64_t(batch) * num_q_heads : 0);
+  a.whole_rows = whole_rows ? 1 : 0;
+  a.whole_row0 = int64_t(pl.balanced_wgs) * 2 * num_q_heads;
   a.part_ml = a.part_o ? a.part_o + n_parts * head_dim : nullptr;
   a.seq_first_tile =
       balanced && a.part_o ? reinterpret_cast<int32_t*>(a.part_ml + n_parts * 2) : nullptr;

@@ -250,6 +250,8 @@ def gqa_decode_paged_fn(
             code, splits, _lib.stream_handle(dev)))
         width -= prefix // page_size
     _, _, ws_bytes = decode_plan(b, h_q, h_kv, d, page_size, width, split_tokens)
+    if prefix:
+        ws_bytes += b * h_q * (d + 2) * 4  # whole sequences' rows, folded with the prefix parts
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
     table_width = block_table.shape[1]
     args = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
