@@ -46,8 +46,8 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
 
 # Where attending a shared prefix once (prefill pass over the prefix, suffix decode, merge) beats
 # the plain decode reading the prefix pages per sequence (cache-keeping policy: they hit in
-# L2/MALL): the pass has a fixed cost of ~30-75 us, so it needs enough sequences and prefix.
-_PREFIX_MIN_BATCH, _PREFIX_MIN_TOKENS = 8, 131072
+# L2/MALL): the pass has a fixed cost of ~30-50 us, so it needs enough sequences and prefix.
+_PREFIX_MIN_BATCH, _PREFIX_MIN_TOKENS = 4, 131072
 
 
 @functools.lru_cache(maxsize=256)
@@ -196,10 +196,10 @@ def gqa_decode_paged_fn(
             tolerance of the plain call; bitwise the same for shared and private prefix pages.
             MFMA variant only.
         prefix_pass: keyword-only, with ``shared_prefix_tokens``: "auto" attends the prefix once
-            only where that is faster than the plain decode, i.e. for at least 8 sequences and
+            only where that is faster than the plain decode, i.e. for at least 4 sequences and
             B x P >= 131,072 prefix tokens (measured against the plain call with the
-            cache-keeping policy: the prefix pass wins from 16 sequences at an 8k prefix, from 64
-            at 2k and from 8 at 32k); below that the call is the plain decode, bitwise. "always"
+            cache-keeping policy: the prefix pass wins from 16 sequences at an 8k prefix, from 32
+            at 2k and from 4 at 32k); below that the call is the plain decode, bitwise. "always"
             takes the prefix pass for any batch.
         append: keyword-only ``(key, value, slot_mapping)``, the decode step's new token per
             sequence (key/value [B, H_kv, D] in q's dtype, slot_mapping [B] int32 with
