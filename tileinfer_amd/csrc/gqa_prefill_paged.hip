@@ -158,6 +158,15 @@ __device__ __forceinline__ int block_key_end(const PrefillArgs& a, const SeqExte
   return k_end < 0 ? 0 : k_end;
 }
 
+// Keys the rows [r0, r0 + rows) of a sequence's (token, query head) rows can see (row = token *
+// group + head): j < kv_len, and j <= offset + the last row's token under the causal mask.
+__device__ __forceinline__ int rows_key_end(const PrefillArgs& a, const SeqExtent& s, int r0,
+                                            int rows) {
+  const int last_tok = (r0 + min(rows, s.q_len * a.group - r0) - 1) / a.group;
+  const int k_end = a.causal ? min(s.kv_len, s.offset + last_tok + 1) : s.kv_len;
+  return k_end < 0 ? 0 : k_end;
+}
+
 // Balanced schedule. A unit is (KV head, sequence, query block); its work is kUnitCost plus its key
 // tiles (the fixed part prices a unit's start-up and epilogue in tiles). Units are concatenated KV
 // head major, then by (sequence, query block) "pair", and workgroup i takes work [i * chunk,
@@ -368,8 +377,11 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   // The sub-tile this wave loads (kKT / W rows per wave, inside one sub-tile).
   const int my_sub = (min(wave, LW - 1) * (kKT / LW)) / 16;
 
-  // The current unit (uniform) and this lane's C rows of it; the key split of the unit.
-  int b = 0, kvh = 0, qb0 = 0, split = 0;
+  // The current unit (uniform) and this lane's C rows of it; the key split of the unit. A unit's
+  // rows are the sequence's (token, query head) rows [qr0, qr0 + ROWS) (row = token * G + head):
+  // per-unit workgroups take ROWS consecutive rows whether or not they start a token; balanced
+  // units are whole query blocks of tq tokens (qr0 = block * tq * G).
+  int b = 0, kvh = 0, qr0 = 0, split = 0;
   SeqExtent sx;
   const int32_t* bt_row = a.block_table;
   int wave_last_key = 0, wave_first_key = 0;
@@ -631,7 +643,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     pv(sv, k0, pop);
   };
 
-  // Attention of unit (b, kvh, qb0) over its key tiles [t0, t1): leaves the unnormalised o and
+  // Attention of unit (b, kvh, qr0) over its key tiles [t0, t1): leaves the unnormalised o and
   // the per-lane m_run / l_run. Uniform over the workgroup.
   auto run_unit = [&](int t0, int t1) __attribute__((always_inline)) {
     sx = seq_extent(a, b);
@@ -639,15 +651,17 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     sx.q_len = __builtin_amdgcn_readfirstlane(sx.q_len);
     sx.kv_len = __builtin_amdgcn_readfirstlane(sx.kv_len);
     sx.offset = __builtin_amdgcn_readfirstlane(sx.offset);
-    const int tq = min(a.tq, sx.q_len - qb0);
+    // Rows of the unit: ROWS (per-unit) or its query block's tokens (balanced), clipped to the
+    // sequence's rows.
+    const int ur = min(a.balanced_wgs > 0 ? a.tq * G : ROWS, sx.q_len * G - qr0);
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const int rho = wave * 16 * C + 16 * c + n;
-      const int tok = rho / G;
-      const int hh = rho - tok * G;
-      row_ok[c] = tok < tq;
-      q_pos[c] = a.causal ? sx.offset + qb0 + tok : INT32_MAX;
-      const uint16_t* qrow = a.q + int64_t(sx.q_start + qb0 + tok) * a.q_st +
+      const int tok = (qr0 + rho) / G;  // token of the row within the sequence
+      const int hh = qr0 + rho - tok * G;
+      row_ok[c] = rho < ur;
+      q_pos[c] = a.causal ? sx.offset + tok : INT32_MAX;
+      const uint16_t* qrow = a.q + int64_t(sx.q_start + tok) * a.q_st +
                              int64_t(kvh * G + hh) * a.q_sh + 8 * g;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
@@ -660,9 +674,9 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     }
     // Under the causal mask, keys past wave_last_key are masked for every row of the wave and
     // keys up to wave_first_key are visible to all of them.
-    const int wave_tok = min(tq - 1, ((wave + 1) * 16 * C - 1) / G);
-    wave_last_key = a.causal ? sx.offset + qb0 + wave_tok : INT32_MAX;
-    wave_first_key = a.causal ? sx.offset + qb0 + (wave * 16 * C) / G : INT32_MAX;
+    const int wave_row = min(ur - 1, (wave + 1) * 16 * C - 1);
+    wave_last_key = a.causal ? sx.offset + (qr0 + wave_row) / G : INT32_MAX;
+    wave_first_key = a.causal ? sx.offset + (qr0 + wave * 16 * C) / G : INT32_MAX;
     bt_row = a.block_table + int64_t(b) * a.bt_stride;
     const int cnt = t1 - t0;
     if (cnt > 0) load_ids(t0 * kKT);
@@ -714,10 +728,10 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       const float l_tot = row_group_sum(l_run[c]);
       if (!row_ok[c]) continue;
       const int rho = wave * 16 * C + 16 * c + n;
-      const int tok = rho / G;
-      const int hh = rho - tok * G;
+      const int tok = (qr0 + rho) / G;
+      const int hh = qr0 + rho - tok * G;
       if (a.uo) {  // uniform: unnormalised rows for a later merge (slot of the key split)
-        const int64_t r = (int64_t(split) * a.total_q + sx.q_start + qb0 + tok) * a.hq + kvh * G + hh;
+        const int64_t r = (int64_t(split) * a.total_q + sx.q_start + tok) * a.hq + kvh * G + hh;
 #pragma unroll
         for (int dt = 0; dt < NT; ++dt) {
           *reinterpret_cast<f32x4*>(a.uo + r * D + 16 * dt + 4 * g) = o[c][dt];
@@ -729,10 +743,10 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
         continue;
       }
       uint16_t* orow =
-          a.out + int64_t(sx.q_start + qb0 + tok) * a.o_st + int64_t(kvh * G + hh) * a.o_sh;
+          a.out + int64_t(sx.q_start + tok) * a.o_st + int64_t(kvh * G + hh) * a.o_sh;
       const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
       // Lane (n, g) holds d = 16 dt + 4g .. +3 of its row in o[c][dt].
-      const uint16_t* grow = a.gate ? a.gate + int64_t(sx.q_start + qb0 + tok) * a.gate_st +
+      const uint16_t* grow = a.gate ? a.gate + int64_t(sx.q_start + tok) * a.gate_st +
                                           int64_t(kvh * G + hh) * a.gate_sh
                                     : nullptr;
 #pragma unroll
@@ -786,10 +800,10 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     kvh = blockIdx.x;
     b = blockIdx.z / a.key_splits;
     split = blockIdx.z - b * a.key_splits;
-    qb0 = (gridDim.y - 1 - blockIdx.y) * a.tq;
+    qr0 = (gridDim.y - 1 - blockIdx.y) * ROWS;
     const SeqExtent s0 = seq_extent(a, b);
-    if (qb0 >= s0.q_len) return;  // uniform over the workgroup
-    grid_nt = (block_key_end(a, s0, qb0) + kKT - 1) / kKT;
+    if (qr0 >= s0.q_len * G) return;  // uniform over the workgroup
+    grid_nt = (rows_key_end(a, s0, qr0, ROWS) + kKT - 1) / kKT;
     if (a.key_splits > 1) {
       const int per = (grid_nt + a.key_splits - 1) / a.key_splits;
       grid_t0 = min(split * per, grid_nt);
@@ -818,7 +832,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     if (balanced) {
       nt = __builtin_amdgcn_readfirstlane(v.pair_nt[p]);
       b = __builtin_amdgcn_readfirstlane(v.pair_b[p]);
-      qb0 = __builtin_amdgcn_readfirstlane(v.pair_qb[p]) * a.tq;
+      qr0 = __builtin_amdgcn_readfirstlane(v.pair_qb[p]) * a.tq * G;
       // The unit's key tiles occupy work [k_pos, k_pos + nt); this run covers [pos, end).
       const int64_t k_pos = int64_t(kvh) * unit_work +
                             __builtin_amdgcn_readfirstlane(v.pair_pre[p]) + kUnitCost;
@@ -1026,7 +1040,7 @@ int launch_prefill(const PrefillArgs& a, int batch, int max_q, hipStream_t s) {
   const auto kern = a.page_shift >= 0 ? prefill_kernel<D, BAL, true, Tag>()
                                       : prefill_kernel<D, BAL, false, Tag>();
   if constexpr (!BAL) {
-    const dim3 grid(unsigned(a.hkv), unsigned(ceil_div(max_q, a.tq)),
+    const dim3 grid(unsigned(a.hkv), unsigned(ceil_div(int64_t(max_q) * a.group, S::C * S::W * 16)),
                     unsigned(batch * a.key_splits));
     hipLaunchKernelGGL(kern, grid, dim3(64 * S::W), 0, s, a);
     return check_launch("ti_gqa_prefill_paged");
@@ -1175,6 +1189,11 @@ int prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h, const v
   a.max_blocks = max_blocks_per_seq;
   a.causal = causal ? 1 : 0;
   const bool balanced = workspace != nullptr && workspace_bytes > 0;
+  if (!balanced &&
+      ceil_div(int64_t(max_seqlen_q) * a.group, prefill_rows(head_dim, false)) > 65535) {
+    return fail(TI_EUNSUPPORTED, "ti_gqa_prefill_paged: %d query tokens per sequence exceed the "
+                "per-unit grid (65,535 row blocks); pass a workspace", max_seqlen_q);
+  }
   a.tq = prefill_rows(head_dim, balanced) / a.group;
   a.key_tile = prefill_key_tile(head_dim, balanced);
   a.scale_log2 = float(1.4426950408889634 / sqrt(double(head_dim)));
@@ -1294,9 +1313,9 @@ extern "C" int32_t ti_gqa_prefill_key_splits(int32_t total_q, int32_t num_q_head
       (head_dim != 128 && head_dim != 256)) {
     return 1;
   }
-  const int64_t tq = prefill_rows(head_dim, false) / (num_q_heads / num_kv_heads);
-  if (tq <= 0) return 1;
-  const int64_t units = int64_t(num_kv_heads) * ceil_div(total_q, tq);
+  const int64_t units = int64_t(num_kv_heads) *
+                        ceil_div(int64_t(total_q) * (num_q_heads / num_kv_heads),
+                                 prefill_rows(head_dim, false));
   const int64_t tiles = ceil_div(kv_tokens, prefill_key_tile(head_dim, false));
   int64_t s = device_cu_count() / units;
   s = s < ceil_div(tiles, kMinSplitTiles) ? s : ceil_div(tiles, kMinSplitTiles);

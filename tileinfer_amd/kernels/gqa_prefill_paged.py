@@ -57,13 +57,15 @@ _KEY_TILE, _UNIT_COST, _BALANCE_OVERHEAD = 64, 2, 9
 
 
 @functools.lru_cache(maxsize=1024)
-def _per_unit_wins(q_len: int, kv_len: int, causal: bool, h_kv: int, tq: int, wgs: int) -> bool:
-    """One sequence: greedy (heaviest-first) makespan of one workgroup per unit against the
-    balanced schedule's even share plus its overhead."""
+def _per_unit_wins(q_len: int, kv_len: int, causal: bool, h_kv: int, group: int, rows: int,
+                   wgs: int) -> bool:
+    """One sequence: greedy (heaviest-first) makespan of one workgroup per unit (``rows``
+    consecutive (token, query head) rows, row = token * group + head) against the balanced
+    schedule's even share plus its overhead."""
     costs = []
-    for qb0 in range(0, q_len, tq):
-        t = min(tq, q_len - qb0)
-        k_end = min(kv_len, kv_len - q_len + qb0 + t) if causal else kv_len
+    for r0 in range(0, q_len * group, rows):
+        last = (r0 + min(rows, q_len * group - r0) - 1) // group  # the unit's last token
+        k_end = min(kv_len, kv_len - q_len + last + 1) if causal else kv_len
         nt = -(-max(k_end, 0) // _KEY_TILE)
         if nt:
             costs.extend([nt + _UNIT_COST] * h_kv)
@@ -86,9 +88,8 @@ def _choose_per_unit(batch: int, total_q: int, max_q: int, max_k: int | None, ca
     if batch != 1:
         return False
     rows = 128 if d == 256 else 256           # rows of a workgroup (the kernel's launch shape)
-    tq = rows // (h_q // h_kv)
     wgs = torch.cuda.get_device_properties(dev).multi_processor_count
-    return _per_unit_wins(int(total_q), int(max_k), bool(causal), h_kv, tq, wgs)
+    return _per_unit_wins(int(total_q), int(max_k), bool(causal), h_kv, h_q // h_kv, rows, wgs)
 
 
 def _aligned_rows(t: torch.Tensor) -> bool:
