@@ -27,8 +27,9 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_kernel(
     const uint32_t vec = i - tok * row_vecs;
     const int64_t slot = slot_mapping[tok];
     if (slot < 0 || slot >= num_slots) continue;  // -1 padding, or out of range: skip
-    const VecT kx = key[tok * key_stride + vec];
-    const VecT vx = value[tok * value_stride + vec];
+    // The new rows are read once: streaming (nt) loads keep them out of the way of the cache rows.
+    const VecT kx = __builtin_nontemporal_load(key + tok * key_stride + vec);
+    const VecT vx = __builtin_nontemporal_load(value + tok * value_stride + vec);
     k_cache[slot * cache_stride + vec] = kx;
     v_cache[slot * cache_stride + vec] = vx;
   }
