@@ -161,7 +161,7 @@ int ti_copy_blocks(const void* src, void* dst, const int64_t* block_pairs, int64
  *   out          [total_q, num_q_heads, head_dim], written for every row covered by cu_seqlens_q
  *   max_seqlen_q >= every q_len (rows past it are not computed)
  *   workspace    NULL (workspace_bytes ignored): one workgroup per (sequence, KV head, block of
- *                query tokens), one launch; each row's result is then independent of the rest of
+ *                consecutive (token, query head) rows), one launch; each row's result is then independent of the rest of
  *                the batch and of how the prompt was chunked (bitwise). Otherwise, at least
  *                ti_gqa_prefill_workspace_bytes() bytes, 256-byte aligned: a balanced schedule
  *                gives every CU the same number of key tiles (units cut between workgroups are
