@@ -409,21 +409,6 @@ int ti_gqa_decode_paged_noalloc(const void* q, int64_t q_stride_b, int64_t q_str
 /* Size in bytes of the per-GPU static scratch of ti_gqa_decode_paged_noalloc. */
 int64_t ti_gqa_decode_scratch_bytes(void);
 
-/*
- * Measurement probe (no reference counterpart): reads pages [0, n_pages) of `k` and of `v` --
- * page i at byte offset pages[i] * page_bytes (i * page_bytes when `pages` is NULL); ids outside
- * [0, region_pages) are skipped; page_bytes a multiple of 4096 -- with plain
- * 16-byte vector loads and no compute, folding the words into `sink` (workgroups * 256 * 16
- * bytes, contents meaningless). `streaming` selects the `nt` load policy the decode uses for
- * once-read pages; `runs` gives workgroup w the contiguous run [w*c, (w+1)*c) of the page list
- * (c = ceil(n_pages / workgroups), the decode's balanced assignment) instead of a grid-stride
- * loop. The decode's own access pattern without its arithmetic: the bandwidth it reaches is the
- * practical read ceiling the decode is compared with (bench.py --calibrate).
- */
-int ti_hbm_read_probe(const void* k, const void* v, const int32_t* pages, int64_t n_pages,
-                      int64_t page_bytes, int64_t region_pages, int32_t streaming, int32_t runs,
-                      int32_t workgroups, void* sink, void* stream);
-
 /* Text of the last error reported on the calling thread ("" when none). */
 const char* ti_last_error(void);
 

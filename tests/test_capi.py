@@ -223,18 +223,6 @@ def test_noalloc_decode_rejects_plans_beyond_its_scratch():
                                            4, 256, 16, 0, 0, 0, 0, 0, None) == _lib.TI_OK
 
 
-def test_hbm_probe_rejects_partial_sweeps():
-    """The read probe reads whole 4 KiB sweeps per page: other page sizes, or a bad grid, are
-    refused before any launch."""
-    lib = _lib.load()
-    fake = 1 << 20
-    assert lib.ti_hbm_read_probe(fake, fake, None, 4, 6144, 4, 1, 1, 8, fake, None) == _lib.TI_EINVAL
-    assert lib.ti_hbm_read_probe(fake, fake, None, 4, 4096, 4, 1, 1, 0, fake, None) == _lib.TI_EINVAL
-    assert lib.ti_hbm_read_probe(fake + 8, fake, None, 4, 4096, 4, 1, 1, 8, fake,
-                                 None) == _lib.TI_EINVAL
-    assert lib.ti_hbm_read_probe(None, None, None, 0, 4096, 0, 1, 1, 8, None, None) == _lib.TI_OK
-
-
 def test_fused_append_decode_argument_errors_without_device():
     """ti_gqa_decode_paged_append refuses bad append operands on the host, before anything is
     launched (stand-in device addresses, never dereferenced: every call below fails first)."""

@@ -359,6 +359,44 @@ def test_swap_pool_exhaustion_and_free_while_swapped():
     assert m.host_free == [0] and m.block_manager.num_free_blocks == 10
 
 
+def test_deallocate_swapped_sequence_directly_leaves_other_blocks_alone():
+    """The reference scheduler calls block_manager.deallocate itself (engine/scheduler.py:66,
+    228, 291). A swapped-out table holds -1 at swapped positions; those hold no device block and
+    must not wrap to the pool's last block."""
+    m = PagedKVManager(4, 16, num_host_blocks=2)
+    a = Sequence(list(range(32)))
+    m.admit(a)                                   # blocks 0, 1
+    other = Sequence([7] * 32)
+    m.admit(other)                               # blocks 2, 3 (3 is the pool's last id)
+    assert other.block_table == [2, 3]
+    bm = m.block_manager
+    assert m.swap_out(a, max_blocks=1) == [(0, 0)]
+    assert a.block_table == [-1, 1]
+    counts = bm.ref_counts.copy()
+    freed = bm.deallocate(a)
+    assert freed == [1]
+    assert bm.ref_counts[3] == counts[3] == 1 and bm.ref_counts[2] == 1
+    assert -1 not in bm.free_block_ids and sorted(bm.free_block_ids) == [0, 1]
+    assert bm.allocate_block() == 1              # LIFO: the last freed block comes back first
+    assert bm.allocate_block() == 0
+
+
+def test_block_ids_outside_the_pool_are_refused():
+    bm = BlockManager(4, 16)
+    s = seq(16)
+    bm.allocate(s)
+    for bad in ([-1], [4], [0, 9]):
+        with pytest.raises(ValueError, match="outside the pool"):
+            bm._drop(bad)
+        t = seq(16)
+        with pytest.raises(ValueError, match="outside the pool"):
+            bm.share_blocks(t, bad)
+        assert t.block_table == []
+    with pytest.raises(ValueError, match="outside the pool"):
+        bm.release(-1)
+    assert bm.ref_counts.tolist() == [1, 0, 0, 0] and bm.num_free_blocks == 3
+
+
 # ----------------------------------------------------------------------------- prefix index: races
 
 

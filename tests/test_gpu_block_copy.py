@@ -129,3 +129,56 @@ def test_swap_out_in_keeps_decode_bitwise(dev):
     swap_blocks(host, kv, torch.tensor(back, dtype=torch.int64))
     torch.cuda.synchronize()
     assert torch.equal(bits(decode()), bits(ref))
+
+
+def test_config5_swap_full_size(dev):
+    """Config 5's swap at its stated size: 32 of the 128 sequences (a quarter) swap out their 32
+    unique blocks each -- 1,024 blocks x 16 layers x K and V, 1 GiB -- through
+    PagedKVManager.swap_out and one swap_blocks launch, the freed blocks are overwritten (another
+    sequence's data), and the sequences swap back in through swap_in and one launch into the
+    blocks the pool hands out. The round trip is bit-exact and every layer's decode of the whole
+    batch (shared prefix included) is bitwise what it was before the swap."""
+    from tileinfer_amd.workloads import config5_managed
+
+    layers = 16
+    say("config 5 swap, full size: 128 sequences, 16 layers, 1,024 blocks each way")
+    mb = config5_managed(dev, layers=layers)
+    m, kv = mb.manager, mb.kv
+    assert kv.shape == (2, layers, 4608, 16, 4, 256)
+    table, seqlen = mb.tables()
+
+    def decode_all(tbl, sl):
+        outs = []
+        for l in range(layers):
+            _, _, kp, vp = layer_views(kv, l)
+            outs.append(gqa_decode_paged_fn(mb.q[l], kp, vp, tbl, sl, 16))
+        return torch.stack(outs)
+
+    ref = decode_all(table, seqlen)
+    victims = mb.seqs[::4]
+    pairs_out = [p for s in victims for p in m.swap_out(s)]
+    assert len(pairs_out) == 1024 and len(victims) == 32
+    assert all(s.block_table[:512] == mb.seqs[0].block_table[:512] for s in victims)
+    old_ids = torch.tensor([b for b, _ in pairs_out], dtype=torch.int64, device=dev)
+    before = kv[:, :, old_ids].clone()
+    host = torch.empty((2, layers, 1024, 16, 4, 256), dtype=torch.bfloat16, pin_memory=True)
+    swap_blocks(kv, host, torch.tensor(pairs_out, dtype=torch.int64))
+    torch.cuda.synchronize()
+    slots = torch.tensor([h for _, h in pairs_out], dtype=torch.int64)
+    assert torch.equal(bits(host[:, :, slots]), bits(before.cpu()))
+    # The freed blocks now belong to someone else: overwrite them.
+    assert m.block_manager.num_free_blocks == 1024
+    kv[:, :, old_ids] = torch.randn(before.shape, generator=torch.Generator(device=dev)
+                                    .manual_seed(99), device=dev).to(torch.bfloat16)
+    pairs_in = [p for s in victims for p in m.swap_in(s)]
+    assert len(pairs_in) == 1024 and m.block_manager.num_free_blocks == 0
+    swap_blocks(host, kv, torch.tensor(pairs_in, dtype=torch.int64))
+    torch.cuda.synchronize()
+    # Host slot h went out from device block b and came back into block n: bit-exact.
+    out_of = {h: i for i, (_, h) in enumerate(pairs_out)}
+    order = torch.tensor([out_of[h] for h, _ in pairs_in], dtype=torch.int64, device=dev)
+    new_ids = torch.tensor([n for _, n in pairs_in], dtype=torch.int64, device=dev)
+    assert torch.equal(bits(kv[:, :, new_ids]), bits(before[:, :, order]))
+    table2, seqlen2 = mb.tables()
+    assert not bool((table2 < 0).any())
+    assert torch.equal(bits(decode_all(table2, seqlen2)), bits(ref))

@@ -39,9 +39,9 @@ def _oracle_rows(q, k_cache, v_cache, table, seqlen, rows):
 
 
 def test_config3_layer_full_size(dev):
-    """Batch 64 x 32,768 tokens over a randomly permuted 131,072-block pool (one layer, 8 GiB per
-    K and per V): default balanced plan (256 workgroups of 8,192 tokens) and the configured
-    2,048-token partitions, 4 sampled sequences against the oracle."""
+    """Batch 64 x 32,768 tokens over a randomly permuted 131,072-block pool (one layer: 4 GiB
+    of K and 4 GiB of V): default balanced plan (256 workgroups of 8,192 tokens) and the
+    configured 2,048-token partitions, 4 sampled sequences against the oracle."""
     b, ctx = 64, 32768
     nb = b * ctx // BLOCK
     say(f"config3 layer: batch {b} x ctx {ctx}, {nb} blocks")

@@ -52,3 +52,70 @@ def test_noalloc_matches_workspace_entry_two_calls(split, dev):
         torch.cuda.synchronize()
         assert torch.cuda.memory_allocated(dev) == before
         assert torch.equal(bits(out), bits(ref)), name
+
+
+@pytest.mark.parametrize("variant,kv_reuse,split", [("auto", False, None), ("auto", True, None),
+                                                   ("scalar", False, 2048)])
+def test_noalloc_python_wrapper_matches_decode_fn(variant, kv_reuse, split, dev):
+    """gqa_decode_paged_noalloc (the Python side of the entry point) marshals the same call as
+    gqa_decode_paged_fn: bitwise equal output, into the caller's `out`, for the variant, cache
+    policy and split flags, and with a table one column wide (stride passed as is)."""
+    from tileinfer_amd.kernels.gqa_decode_paged import gqa_decode_paged_noalloc
+
+    big = _on(make_step([4000, 7000, 33, 0, 12000, 5000, 9000, 1] * 2, pool=4800, seed=43), dev)
+    narrow = _on(make_step([16, 9, 1], pool=8, seed=44), dev)
+    assert narrow.block_table.shape[1] == 1
+    for name, step in (("batch 16", big), ("one-column table", narrow)):
+        say(f"no-alloc wrapper {name}: variant={variant} kv_reuse={kv_reuse} split={split}")
+        args = (step.q, step.k_cache, step.v_cache, step.block_table, step.seqlen, 16)
+        ref = gqa_decode_paged_fn(*args, split_tokens=split, variant=variant, kv_reuse=kv_reuse)
+        out = torch.full_like(step.q, float("nan"))
+        torch.cuda.synchronize()
+        before = torch.cuda.memory_allocated(dev)
+        got = gqa_decode_paged_noalloc(*args, out=out, split_tokens=split, variant=variant,
+                                       kv_reuse=kv_reuse)
+        torch.cuda.synchronize()
+        assert got is out and torch.cuda.memory_allocated(dev) == before
+        assert torch.equal(bits(out), bits(ref)), name
+
+
+def test_noalloc_python_wrapper_refusals(dev):
+    """The wrapper refuses, rather than copies, what the entry point cannot take: unaligned q
+    rows, a strided table or lengths, and an `out` of the wrong shape, dtype, device or layout.
+    Nothing is launched for a refused call (`out` keeps its contents)."""
+    from tileinfer_amd.kernels.gqa_decode_paged import gqa_decode_paged_noalloc
+
+    step = _on(make_step([100, 40], pool=16, seed=45), dev)
+    q, kc, vc, table, seqlen = step.q, step.k_cache, step.v_cache, step.block_table, step.seqlen
+    out = torch.zeros_like(q)
+    flat = torch.empty(q.numel() + 1, dtype=q.dtype, device=dev)
+    q_unaligned = flat[1:].view_as(q).copy_(q)
+    table_wide = torch.zeros((table.shape[0], 2 * table.shape[1]), dtype=torch.int32, device=dev)
+    table_strided = table_wide[:, ::2]
+    table_strided.copy_(table)
+    seqlen_strided = torch.zeros(2 * seqlen.numel(), dtype=torch.int32, device=dev)[::2]
+    seqlen_strided.copy_(seqlen)
+    cases = [
+        ("unaligned q", (q_unaligned, kc, vc, table, seqlen), out, "16-byte aligned"),
+        ("strided table", (q, kc, vc, table_strided, seqlen), out, "unit-stride"),
+        ("strided lengths", (q, kc, vc, table, seqlen_strided), out, "unit-stride"),
+        ("out shape", (q, kc, vc, table, seqlen), torch.zeros_like(q[:1]), "out must be"),
+        ("out dtype", (q, kc, vc, table, seqlen), torch.zeros_like(q, dtype=torch.float16),
+         "out must be"),
+        ("out on the host", (q, kc, vc, table, seqlen), torch.zeros_like(q, device="cpu"),
+         "out must be"),
+        ("out strided", (q, kc, vc, table, seqlen),
+         torch.zeros((q.shape[1], q.shape[0], q.shape[2]), dtype=q.dtype,
+                     device=dev).transpose(0, 1), "out must be"),
+    ]
+    for name, args, o, msg in cases:
+        say(f"no-alloc wrapper refusal: {name}")
+        sentinel = o.clone()
+        with pytest.raises(ValueError, match=msg):
+            gqa_decode_paged_noalloc(*args, 16, out=o)
+        torch.cuda.synchronize()
+        assert torch.equal(bits(o), bits(sentinel)), name
+    # The same operands, made valid, run.
+    ref = gqa_decode_paged_fn(q, kc, vc, table, seqlen, 16)
+    gqa_decode_paged_noalloc(q, kc, vc, table, seqlen, 16, out=out)
+    assert torch.equal(bits(out), bits(ref))

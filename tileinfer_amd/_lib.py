@@ -90,8 +90,6 @@ SIGNATURES = {
                                                    _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32,
                                                    _c_i32, _c_vp]),
     "ti_gqa_decode_scratch_bytes": (ctypes.c_int64, []),
-    "ti_hbm_read_probe": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i32,
-                                         _c_i32, _c_i32, _c_vp, _c_vp]),
     "ti_last_error": (ctypes.c_char_p, []),
     "ti_abi_version": (ctypes.c_int32, []),
 }

@@ -18,7 +18,9 @@ Two fixes. ``may_append``: the reference allocates only when ``len(seq) % block_
 token early, and so never gives the first decode token of a prompt whose length is a multiple of
 the block size a slot (engine/block_manager.py:107-117); here it also allocates while the table
 holds fewer slots than tokens, and ``can_append`` counts both. Releasing a block that is already
-free raises instead of corrupting the pool.
+free, or an id outside ``[0, num_blocks)``, raises instead of corrupting the pool (numpy would
+wrap a -1 to the last block). ``deallocate`` skips negative table entries: they are positions
+that hold no device block (swapped out to host memory), the way the device tables mark them.
 """
 from __future__ import annotations
 
@@ -112,12 +114,19 @@ class BlockManager:
             for block_id in ids:
                 self.on_block_freed(block_id)
 
+    def _check_ids(self, arr: np.ndarray) -> None:
+        bad = (arr < 0) | (arr >= self.num_blocks)
+        if bad.any():
+            raise ValueError(f"block id {int(arr[bad][0])} is outside the pool "
+                             f"[0, {self.num_blocks})")
+
     def _drop(self, ids: list[int]) -> list[int]:
         """Drop one reference per listing of each id, walking the list last to first; returns the
         ids that became free, in the order they go back on the stack."""
         if not ids:
             return []
         arr = np.asarray(ids[::-1], dtype=np.int64)
+        self._check_ids(arr)
         uniq, mult = np.unique(arr, return_counts=True)
         short = self.ref_counts[uniq] < mult
         if short.any():
@@ -150,6 +159,7 @@ class BlockManager:
         if seq.block_table:
             raise ValueError(f"sequence {seq.seq_id} already has blocks")
         arr = np.asarray(block_ids, dtype=np.int64)
+        self._check_ids(arr)
         if arr.size and (self.ref_counts[arr] <= 0).any():
             bad = int(arr[self.ref_counts[arr] <= 0][0])
             raise ValueError(f"cannot share free block {bad}")
@@ -165,8 +175,10 @@ class BlockManager:
         seq.block_table.extend(self._take(max(0, seq.num_blocks - len(seq.block_table))))
 
     def deallocate(self, seq: Sequence) -> list[int]:
-        """Drop the sequence's references; return the ids whose count reached 0 (freed)."""
-        freed = self._drop(seq.block_table)
+        """Drop the sequence's references; return the ids whose count reached 0 (freed).
+        Negative entries (positions swapped out to host memory) hold no device block and are
+        skipped."""
+        freed = self._drop([b for b in seq.block_table if b >= 0])
         seq.block_table.clear()
         seq.table_changed()
         return freed

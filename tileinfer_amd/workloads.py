@@ -206,6 +206,61 @@ def config5(seed: int = 1005, device="cpu", batch: int = 128, prefix: int = 8192
 
 
 @dataclass
+class ManagedBatch:
+    """A batch whose blocks a ``PagedKVManager`` owns, over an all-layer cache slab."""
+    manager: "object"           # tileinfer_amd.engine.PagedKVManager
+    seqs: list                  # [Sequence]
+    kv: torch.Tensor            # [2, L, pool, BLOCK, HKV, D]
+    q: torch.Tensor             # [L, B, HQ, D]
+
+    def tables(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """(block_table [B, W] int32 with -1 padding, seqlen [B] int32) on the cache's device,
+        built from the sequences' current tables (W = the longest)."""
+        w = max(len(s.block_table) for s in self.seqs)
+        table = torch.full((len(self.seqs), w), -1, dtype=torch.int32)
+        for i, s in enumerate(self.seqs):
+            table[i, :len(s.block_table)] = torch.tensor(s.block_table, dtype=torch.int32)
+        seqlen = torch.tensor([s.num_tokens for s in self.seqs], dtype=torch.int32)
+        return table.to(self.kv.device), seqlen.to(self.kv.device)
+
+
+def config5_managed(device="cuda", layers: int = 16, batch: int = 128, prefix: int = 8192,
+                    suffix: int = 512, seed: int = 1005, swap_fraction: float = 0.25,
+                    dtype=torch.bfloat16) -> ManagedBatch:
+    """Config 5 set up the way a serving engine gets there: sequence 0's prompt is computed and
+    its whole-block prefix recorded in the prefix cache; the other sequences share those
+    ``prefix / 16`` blocks through the cache hit (``share_blocks``, refcounted) and own ``suffix
+    / 16`` blocks each. The pool holds exactly the physical blocks (512 + 128 x 32 = 4,608) and a
+    pinned host pool the blocks of ``swap_fraction`` of the sequences (1,024). All ``layers``
+    layers' K/V are N(0,1) values (the stand-in for the prefill), q one [B, 24, 256] per layer."""
+    from .engine import PagedKVManager, Sequence
+    from .engine.kv_layout import allocate_kv_cache
+
+    pb, sb = prefix // BLOCK, suffix // BLOCK
+    pool = pb + batch * sb
+    host_blocks = int(batch * swap_fraction) * sb
+    m = PagedKVManager(pool, BLOCK, enable_prefix_caching=True, num_host_blocks=host_blocks)
+    shared = list(range(prefix))
+    seqs = []
+    for i in range(batch):
+        own = [prefix + 1 + i * suffix + j for j in range(suffix)]
+        s = Sequence(shared + own)
+        if not m.admit(s):
+            raise RuntimeError("config5_managed: pool too small")
+        if i == 0:
+            m.finish_chunk(s, prefix)            # whole-block prefix recorded here
+        m.finish_chunk(s, s.num_tokens - s.num_cached_tokens)
+        seqs.append(s)
+    if any(s.block_table[:pb] != seqs[0].block_table[:pb] for s in seqs[1:]):
+        raise AssertionError("config5_managed: the prefix was not shared")
+    kv = allocate_kv_cache(layers, pool, BLOCK, HKV, HEAD_DIM, device, dtype, zero=False)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    kv.normal_(generator=gen)
+    q = _randn((layers, batch, HQ, HEAD_DIM), gen, device, dtype)
+    return ManagedBatch(manager=m, seqs=seqs, kv=kv, q=q)
+
+
+@dataclass
 class PrefillStep:
     """One attention layer's chunked-prefill inputs: packed query rows over paged K/V.
 
