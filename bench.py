@@ -556,8 +556,10 @@ def other_configs_decode(dev, args) -> dict:
               5: wl.config5}[cfg](device=dev)
         ctx = st.seqlen.tolist()
         nbytes = decode_bytes(ctx)
+        # The unchanged call site's call (model/qwen_36.py:1071-1079 passes no hint): the cache
+        # policy is chosen on the device.
         call = functools.partial(gqa_decode_paged_fn, st.q, st.k_cache, st.v_cache,
-                                 st.block_table, st.seqlen, BLOCK, kv_reuse=cfg == 5)
+                                 st.block_table, st.seqlen, BLOCK)
         us = _time(call, args.steps, args.warmup)
         entry = {"batch": len(ctx), "ctx_sum": sum(ctx), "decode_us": round(us, 2),
                  "decode_GBps_algorithmic": round(nbytes / (us * 1e-6) / 1e9, 1),
@@ -574,8 +576,17 @@ def other_configs_decode(dev, args) -> dict:
                                     st.block_table, st.seqlen, BLOCK,
                                     shared_prefix_tokens=st.meta["prefix_tokens"])
             entry["decode_us_shared_prefix"] = round(_time(pre, args.steps, args.warmup), 2)
-            entry["note"] = ("plain decode with the cache-keeping policy (shared prefix pages hit "
-                             "L2/MALL, so the logical % can exceed 100); shared_prefix: the "
+            for name, reuse in (("decode_us_forced_keep", True), ("decode_us_forced_stream", False)):
+                entry[name] = round(_time(functools.partial(call, kv_reuse=reuse), args.steps,
+                                          args.warmup), 2)
+            out = call()
+            entry["policies_bitwise_equal"] = all(
+                torch.equal(out.view(torch.int16), call(kv_reuse=r).view(torch.int16))
+                for r in (True, False))
+            entry["note"] = ("decode_us: the call with no keywords (cache policy chosen per "
+                             "sequence on the device: the shared prefix pages are kept in "
+                             "L2/MALL, so the logical % can exceed 100); forced_keep / "
+                             "forced_stream: kv_reuse=True / False; shared_prefix: the "
                              "8,192-token prefix attended once for the batch")
         res[f"config{cfg}"] = entry
         del st
@@ -698,17 +709,17 @@ def run_config(cfg: int, args, dev) -> dict:
         key, val, slots = st.k_new, st.v_new, st.slot_mapping
     ctx = st.seqlen.tolist()
     a_us = _time(lambda: store_kvcache(key, val, rows(kc), rows(vc), slots), args.steps, args.warmup)
-    reuse = cfg == 5  # tables alias one prefix: keep K/V cacheable (PagedKVManager.shares_blocks)
+    # No cache-policy hint, as the unchanged call site passes none: chosen on the device.
     d_us = _time(lambda: gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen,
                                              split_tokens=args.split_tokens,
-                                             variant=args.variant, kv_reuse=reuse),
+                                             variant=args.variant),
                  args.steps, args.warmup)
     a_bytes = append_bytes(slots, HKV * HEAD_DIM)
     d_bytes = decode_bytes(ctx)
     # Parity and the CPU reference on this state (the timed append, then decode), before the
     # extra measurements below write elsewhere in the pool.
     out = gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen,
-                              split_tokens=args.split_tokens, variant=args.variant, kv_reuse=reuse)
+                              split_tokens=args.split_tokens, variant=args.variant)
     checks = {"parity": config_parity(cfg, st, key, val, slots, out, dev)}
     if not args.no_cpu_baseline:
         checks["cpu_reference"] = config_cpu_reference(st, key, val, slots)
@@ -732,7 +743,12 @@ def run_config(cfg: int, args, dev) -> dict:
         unique = int(torch.unique(st.block_table).numel())
         stream_us = _time(lambda: gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen,
                                                       split_tokens=args.split_tokens,
-                                                      variant=args.variant), args.steps, args.warmup)
+                                                      variant=args.variant, kv_reuse=False),
+                          args.steps, args.warmup)
+        keep_us = _time(lambda: gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen,
+                                                    split_tokens=args.split_tokens,
+                                                    variant=args.variant, kv_reuse=True),
+                        args.steps, args.warmup)
         # The prefix attended once for the batch (the caller's statement that every sequence
         # shares its first 8192 tokens), against the plain call's output.
         prefix = st.meta["prefix_tokens"]
@@ -743,6 +759,7 @@ def run_config(cfg: int, args, dev) -> dict:
         plain = gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen, kv_reuse=True)
         shared_err = float((shared_fn().float() - plain.float()).abs().max())
         extra = {"decode_us_streaming_policy": round(stream_us, 2),
+                 "decode_us_keep_policy": round(keep_us, 2),
                  "decode_us_shared_prefix": round(shared_us, 2),
                  "decode_GBps_logical_shared_prefix": round(d_bytes / (shared_us * 1e-6) / 1e9, 1),
                  "shared_prefix_tokens": prefix,

@@ -44,10 +44,16 @@ extern "C" {
 #define TI_DECODE_AUTO 0   /* the measured-fastest variant for the shape */
 #define TI_DECODE_MFMA 1   /* query group packed into a 16-row MFMA tile, K/V direct to registers */
 #define TI_DECODE_SCALAR 2 /* K/V pages staged in LDS, fp32 FMA, DPP/shuffle softmax reductions */
-/* Flag OR'd into `variant`: the call's block tables share pages across sequences (prefix caching),
- * so K/V is loaded with the default cache policy and shared pages are served from L2/MALL. Without
- * it K/V is loaded as a once-read stream (`nt`), faster when every page is read once per call. */
+/* Cache policy of the K/V loads. With neither flag (the default) the MFMA variant chooses per
+ * sequence on the device: a sequence whose first block id another sequence of the batch also has
+ * in its first column (prefix caching shares whole-block chains from there) loads with the default
+ * cache policy, so the pages the other sequences read again are served from L2/MALL; every other
+ * sequence loads its pages as a once-read stream (`nt`), faster when a page is read once per call.
+ * (Batches above 2,048 sequences stream.) TI_DECODE_REUSE_KV forces the default policy for every
+ * page, TI_DECODE_STREAM_KV forces `nt`; the scalar variant streams unless REUSE_KV is given.
+ * Results are bitwise the same under every policy. */
 #define TI_DECODE_REUSE_KV 0x10
+#define TI_DECODE_STREAM_KV 0x20
 
 /*
  * Slot-mapped K/V append: for every i in [0, n_tokens) with 0 <= slot_mapping[i] < num_slots,
@@ -111,7 +117,7 @@ int ti_gqa_decode_plan(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
  *   workspace    >= workspace_bytes from ti_gqa_decode_plan with the same arguments (may be NULL
  *                when that is 0); contents need no initialisation.
  *   split_tokens as in ti_gqa_decode_plan; variant one of TI_DECODE_AUTO/MFMA/SCALAR, optionally
- *                OR'd with TI_DECODE_REUSE_KV.
+ *                OR'd with TI_DECODE_REUSE_KV or TI_DECODE_STREAM_KV.
  */
 int ti_gqa_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
                         const void* v_cache, const int32_t* block_table, int64_t block_table_stride,

@@ -109,8 +109,9 @@ def test_config5_full_batch(dev):
 
     plain = call(shared, kv_reuse=True)
     assert torch.equal(bits(plain), bits(call(private, kv_reuse=True)))
-    assert torch.equal(bits(plain), bits(call(shared)))
-    assert torch.equal(bits(plain), bits(call(private)))
+    for reuse in (None, False):  # chosen on the device (keep here), and forced streaming
+        assert torch.equal(bits(plain), bits(call(shared, kv_reuse=reuse)))
+        assert torch.equal(bits(plain), bits(call(private, kv_reuse=reuse)))
     pre = call(shared, shared_prefix_tokens=8192)
     assert torch.equal(bits(pre), bits(call(private, shared_prefix_tokens=8192)))
     rows = [0, 1, 63, 64, 127]

@@ -105,7 +105,7 @@ def test_shared_vs_private_prefix_bitwise(dev):
     private = config5(batch=8, device=dev, shared=False)
     o1 = None
     for variant in VARIANTS:
-        for reuse in (False, True):
+        for reuse in (None, False, True):
             a = gqa_decode_paged_fn(shared.q, shared.k_cache, shared.v_cache, shared.block_table,
                                     shared.seqlen, variant=variant, kv_reuse=reuse)
             b = gqa_decode_paged_fn(private.q, private.k_cache, private.v_cache,
@@ -125,6 +125,41 @@ def test_shared_vs_private_prefix_bitwise(dev):
                         v_cache=shared.v_cache[pages].cpu())
         ref, _, _ = cpu_step(sub, append=False)
         assert_decode_close(o1[i:i + 1], ref)
+
+
+def test_cache_policy_chosen_on_device_bitwise(dev):
+    """The default call picks each sequence's cache policy on the device (a first block another
+    sequence also starts with -> keep, else stream). Whatever it picks, the output is bitwise the
+    forced-keep and forced-stream output: two groups sharing different prefixes, private rows,
+    the runner's graph-padding rows (context 1, all -1), both plans; and at the batch sizes on
+    either side of the device set's limit (2,048 sequences: every first block shared; 2,049: no
+    set, every sequence streams)."""
+    say("decode cache policy: device choice vs forced, two prefix groups + padding rows")
+    step = make_step([700, 900, 260, 1100, 640, 850, 480, 2000, 33, 1, 1, 1], pool=640, seed=17)
+    table = step.block_table.clone()
+    table[1:4, :16] = table[0, :16]          # group A: 256 tokens of shared pages
+    table[5:7, :8] = table[4, :8]            # group B: 128 tokens
+    table[9:] = -1                           # graph-padding rows
+    q, kc, vc = step.q.to(dev), step.k_cache.to(dev), step.v_cache.to(dev)
+    tb, sl = table.to(dev), step.seqlen.to(dev)
+    for split in (None, 512):
+        outs = [gqa_decode_paged_fn(q, kc, vc, tb, sl, split_tokens=split, kv_reuse=r)
+                for r in (None, True, False)]
+        assert torch.equal(bits(outs[0]), bits(outs[1])), split
+        assert torch.equal(bits(outs[0]), bits(outs[2])), split
+        assert not bool(outs[0][9:].view(torch.int16).any())
+    ref = ref_gqa_decode_paged(step.q[:9], step.k_cache, step.v_cache, table[:9],
+                               step.seqlen[:9], 16)
+    assert_decode_close(outs[0][:9], ref)
+    for b, share in ((2048, True), (2049, False)):
+        say(f"decode cache policy at batch {b}")
+        big = make_step([17] * b, pool=2 * b, seed=18, device=dev)
+        t = big.block_table.clone()
+        if share:
+            t[:, 0] = t[0, 0]
+        res = [gqa_decode_paged_fn(big.q, big.k_cache, big.v_cache, t, big.seqlen, kv_reuse=r)
+               for r in (None, True, False)]
+        assert torch.equal(bits(res[0]), bits(res[1])) and torch.equal(bits(res[0]), bits(res[2]))
 
 
 def test_block_permutation_and_padding_bitwise(dev):

@@ -77,6 +77,7 @@ def test_noalloc_python_wrapper_matches_decode_fn(variant, kv_reuse, split, dev)
         torch.cuda.synchronize()
         assert got is out and torch.cuda.memory_allocated(dev) == before
         assert torch.equal(bits(out), bits(ref)), name
+        del got, out, ref  # the next case's count starts without them
 
 
 def test_noalloc_python_wrapper_refusals(dev):

@@ -25,6 +25,7 @@ TI_DECODE_AUTO = 0
 TI_DECODE_MFMA = 1
 TI_DECODE_SCALAR = 2
 TI_DECODE_REUSE_KV = 0x10
+TI_DECODE_STREAM_KV = 0x20
 ABI_VERSION = 7
 
 # Every symbol declared in include/tileinfer_amd.h, with its ctypes signature.

@@ -80,6 +80,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t* base
 // (config 5: 450 us with kPolicyKeep against 770 us with kPolicyStream).
 constexpr int kPolicyKeep = 0;
 constexpr int kPolicyStream = 2;
+// Chosen per sequence on the device (decode_mfma_kernel): kPolicyKeep when another sequence of the
+// batch starts with the same block (prefix caching shares whole-block chains from a table's first
+// column, so that finds every sequence whose pages other sequences also read), else kPolicyStream.
+constexpr int kPolicyAuto = -1;
 
 template <int POL>
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset) {

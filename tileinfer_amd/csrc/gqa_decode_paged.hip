@@ -55,6 +55,54 @@ struct Tile {
   int rows;             // tokens of the tile that exist (uniform)
 };
 
+// Issues one tile's K and V loads (MFMA operand layout) with cache policy P.
+template <int D, int P>
+__device__ __forceinline__ void issue_tile(Tile<D>& T, __amdgpu_buffer_rsrc_t rk,
+                                           __amdgpu_buffer_rsrc_t rv, uint32_t lane_k,
+                                           uint32_t lane_v, uint32_t row_bytes) {
+#pragma unroll
+  for (int kk = 0; kk < D / 32; ++kk) T.k[kk] = buffer_load16<P>(rk, lane_k + 64 * kk);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int c = 0; c < D / 128; ++c) T.v[r][c] = buffer_load16<P>(rv, lane_v + r * row_bytes + 256 * c);
+  }
+}
+
+// The batch's first-column block ids in an LDS hash set with a count per id, so that a sequence
+// can ask whether another sequence starts with the same block (kPolicyAuto). Open addressing with
+// linear probing over `slots` (a power of two, at least twice the ids inserted).
+constexpr int kShareSlots = 4096;
+constexpr int kShareMaxBatch = kShareSlots / 2;
+
+__device__ __forceinline__ uint32_t share_hash(int id, int slots) {
+  return (uint32_t(id) * 2654435761u) & uint32_t(slots - 1);
+}
+
+__device__ __forceinline__ void share_insert(int* keys, int* counts, int slots, int id) {
+  uint32_t h = share_hash(id, slots);
+  for (int probe = 0; probe < slots; ++probe) {
+    const int old = atomicCAS(&keys[h], -1, id);
+    if (old == -1 || old == id) {
+      atomicAdd(&counts[h], 1);
+      return;
+    }
+    h = (h + 1) & uint32_t(slots - 1);
+  }
+}
+
+// Count of `id` in the set (uniform: every lane probes the same slots).
+__device__ __forceinline__ int share_count(const int* keys, const int* counts, int slots, int id) {
+  uint32_t h = share_hash(id, slots);
+  for (int probe = 0; probe < slots; ++probe) {
+    const int k = keys[h];
+    if (k == id) return counts[h];
+    if (k == -1) return 0;
+    h = (h + 1) & uint32_t(slots - 1);
+  }
+  return 0;
+}
+
 // Wave-wide inclusive prefix sum.
 __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
 #pragma unroll
@@ -102,6 +150,64 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
   float m_run, l_run, l_tot;
   int tok0, tok1;
 
+  // Cache policy of the current sequence's K/V loads (uniform). kPolicyAuto: the batch's
+  // first-column block ids go into an LDS hash set here, and a sequence whose first block another
+  // sequence also starts with loads with kPolicyKeep (its pages are read again by the others and
+  // are then served from L2/MALL); every other sequence streams. Rows of an empty table (id -1:
+  // the runner's graph padding) and ids outside the cache are left out. A barrier follows before
+  // the first lookup (the balanced scan's, or the one below for fixed splits).
+  bool keep = POL == kPolicyKeep;
+  int share_slots = 0;  // 0: no set (batch too large), every sequence streams
+  int* s_skey = nullptr;
+  int* s_scnt = nullptr;
+  if constexpr (POL == kPolicyAuto) {
+    __shared__ int s_share_key[kShareSlots];
+    __shared__ int s_share_cnt[kShareSlots];
+    s_skey = s_share_key;
+    s_scnt = s_share_cnt;
+    if (batch <= kShareMaxBatch && a.max_blocks > 0) {  // uniform
+      share_slots = 64;
+      while (share_slots < 2 * batch) share_slots <<= 1;
+    }
+  }
+  // One wave fills the set (a wave's LDS operations take effect in order, so its clear precedes
+  // its inserts without a barrier): the last wave, while wave 0 runs the balanced scan, so the
+  // set costs no time on the start-up path; with one wave per workgroup, wave 0 after its scan.
+  // The barrier at the end of the scan (or the one below, for fixed splits) publishes it.
+  auto build_share_set = [&]() {
+    if constexpr (POL == kPolicyAuto) {
+      if (share_slots == 0) return;
+      for (int e = lane; e < share_slots; e += 64) {
+        s_skey[e] = -1;
+        s_scnt[e] = 0;
+      }
+      for (int j0 = 0; j0 < batch; j0 += 8 * 64) {
+        int ids[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {  // the chunk's loads issued together
+          const int j = j0 + 64 * u + lane;
+          ids[u] = j < batch ? a.block_table[int64_t(j) * a.bt_stride] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (uint32_t(ids[u]) < uint32_t(a.num_blocks32)) {
+            share_insert(s_skey, s_scnt, share_slots, ids[u]);
+          }
+        }
+      }
+    }
+  };
+  // Sets `keep` for sequence b from its first block id (loaded by the caller ahead of a barrier).
+  auto choose_policy = [&](int first_id) {
+    if constexpr (POL == kPolicyAuto) {
+      keep = false;
+      const int id = __builtin_amdgcn_readfirstlane(first_id);
+      if (share_slots > 0 && uint32_t(id) < uint32_t(a.num_blocks32)) {
+        keep = __builtin_amdgcn_readfirstlane(share_count(s_skey, s_scnt, share_slots, id)) > 1;
+      }
+    }
+  };
+
   // Loads the 16-token tile at position p into `T`. Every load is issued unconditionally through
   // a buffer descriptor that spans only the tile's rows that exist (in the partition and with a
   // valid block id); rows past it read as zero with no memory access. Branch-free loads keep the
@@ -119,12 +225,11 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     const uint32_t nbytes = rows > 0 ? uint32_t(rows - 1) * row_bytes + D * 2 : 0u;
     const auto rk = make_rsrc(a.k_cache + base, nbytes);
     const auto rv = make_rsrc(a.v_cache + base, nbytes);
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) T.k[kk] = buffer_load16<POL>(rk, lane_k + 64 * kk);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-#pragma unroll
-      for (int c = 0; c < NC; ++c) T.v[r][c] = buffer_load16<POL>(rv, lane_v + r * row_bytes + 256 * c);
+    if constexpr (POL == kPolicyAuto) {
+      if (keep) issue_tile<D, kPolicyKeep>(T, rk, rv, lane_k, lane_v, row_bytes);
+      else issue_tile<D, kPolicyStream>(T, rk, rv, lane_k, lane_v, row_bytes);
+    } else {
+      issue_tile<D, POL>(T, rk, rv, lane_k, lane_v, row_bytes);
     }
     T.rows = rows;
   };
@@ -193,11 +298,15 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     const int page0 = tok0 / a.page_size;
     // The plan keeps every partition within kMaxSplitPages pages; the clamp only guards LDS.
     const int npages = tok1 > tok0 ? min((tok1 - 1) / a.page_size - page0 + 1, kMaxSplitPages) : 0;
+    // The sequence's first block id (cache policy), requested with the partition's block ids.
+    const int first_id =
+        (POL == kPolicyAuto && share_slots > 0 && npages > 0) ? a.block_table[b * a.bt_stride] : -1;
     __syncthreads();  // the previous partition's tiles are done with s_bids
     for (int i = threadIdx.x; i < npages; i += 64 * WPB) {
       s_bids[i] = a.block_table[b * a.bt_stride + page0 + i];
     }
     __syncthreads();
+    choose_policy(first_id);
     // Query group as the B operand of S^T = K . Q^T; rows beyond the group stay zero.
     const uint16_t* qrow = a.q + b * a.q_sb + int64_t(h) * a.q_sh;
 #pragma unroll
@@ -325,6 +434,10 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     const int ctx = seq_len(a, b);
     const int nsplit = (ctx + a.split_tokens - 1) / a.split_tokens;
     if (split >= (nsplit > 0 ? nsplit : 1)) return;  // uniform over the workgroup
+    if constexpr (POL == kPolicyAuto) {
+      if (wave == 0) build_share_set();
+      __syncthreads();
+    }
     const int t0 = split * a.split_tokens;
     run_partition(b, t0, min(t0 + a.split_tokens, ctx));
     if (!head_ok) return;
@@ -336,6 +449,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
   // Balanced: workgroup i takes tiles [i * chunk, (i + 1) * chunk) of the batch's concatenated
   // 16-token tiles. Wave 0 finds the first and last sequence of that run with a prefix scan.
   const int i = blockIdx.y;
+  if (WPB > 1 && wave == WPB - 1) build_share_set();
   if (wave == 0) {
     // Lane l owns sequences [l K, l K + K), K = ceil(batch / 64): it sums their tile counts (the
     // loads issued together, so any batch costs about one memory latency), the lane sums are
@@ -398,6 +512,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
       s_part[3] = s_first;
       s_part[4] = b_last;
     }
+    if (WPB == 1) build_share_set();
   }
   __syncthreads();
   const int T0 = __builtin_amdgcn_readfirstlane(s_part[0]);
@@ -717,14 +832,17 @@ __global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int 
 }
 
 template <int D, typename Tag, int WPB>
-int launch_mfma(const DecodeArgs& a, int batch, bool reuse_kv, hipStream_t stream) {
+int launch_mfma(const DecodeArgs& a, int batch, int policy, hipStream_t stream) {
   const dim3 grid = a.balanced_wgs > 0 ? dim3(a.hkv / WPB, a.balanced_wgs, 1)
                                         : dim3(a.hkv / WPB, a.max_splits, batch);
-  if (reuse_kv) {
+  if (policy == kPolicyKeep) {
     hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyKeep>), grid, dim3(64 * WPB), 0,
                        stream, a, batch);
-  } else {
+  } else if (policy == kPolicyStream) {
     hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyStream>), grid, dim3(64 * WPB), 0,
+                       stream, a, batch);
+  } else {
+    hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyAuto>), grid, dim3(64 * WPB), 0,
                        stream, a, batch);
   }
   return check_launch("ti_gqa_decode_paged (mfma)");
@@ -736,14 +854,14 @@ int launch_mfma(const DecodeArgs& a, int batch, bool reuse_kv, hipStream_t strea
 constexpr int kWideMergeBatch = 4;
 
 template <int D, typename Tag>
-int launch_decode(const DecodeArgs& a, int batch, bool reuse_kv, hipStream_t stream) {
+int launch_decode(const DecodeArgs& a, int batch, int policy, hipStream_t stream) {
   int rc;
   if (a.hkv % 4 == 0) {
-    rc = launch_mfma<D, Tag, 4>(a, batch, reuse_kv, stream);
+    rc = launch_mfma<D, Tag, 4>(a, batch, policy, stream);
   } else if (a.hkv % 2 == 0) {
-    rc = launch_mfma<D, Tag, 2>(a, batch, reuse_kv, stream);
+    rc = launch_mfma<D, Tag, 2>(a, batch, policy, stream);
   } else {
-    rc = launch_mfma<D, Tag, 1>(a, batch, reuse_kv, stream);
+    rc = launch_mfma<D, Tag, 1>(a, batch, policy, stream);
   }
   if (rc != TI_OK) return rc;
   if (a.balanced_wgs > 0 && batch <= kWideMergeBatch) {
@@ -902,10 +1020,14 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
   }
   const int kind = variant & 0xF;
   const bool reuse_kv = (variant & TI_DECODE_REUSE_KV) != 0;
+  const bool stream_kv = (variant & TI_DECODE_STREAM_KV) != 0;
   if ((kind != TI_DECODE_AUTO && kind != TI_DECODE_MFMA && kind != TI_DECODE_SCALAR) ||
-      (variant & ~(0xF | TI_DECODE_REUSE_KV)) != 0) {
+      (variant & ~(0xF | TI_DECODE_REUSE_KV | TI_DECODE_STREAM_KV)) != 0 ||
+      (reuse_kv && stream_kv)) {
     return fail(TI_EINVAL, "ti_gqa_decode_paged: unknown variant/flags 0x%x", variant);
   }
+  // The MFMA kernel's K/V cache policy: forced by a flag, else chosen per sequence on the device.
+  const int policy = reuse_kv ? kPolicyKeep : stream_kv ? kPolicyStream : kPolicyAuto;
   Plan pl;
   int rc = plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq,
                 split_tokens, &pl);
@@ -1027,11 +1149,11 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
     return TI_OK;
   }
   if (head_dim == 256) {
-    return bf16 ? launch_decode<256, Bf16>(a, batch, reuse_kv, s)
-                : launch_decode<256, F16>(a, batch, reuse_kv, s);
+    return bf16 ? launch_decode<256, Bf16>(a, batch, policy, s)
+                : launch_decode<256, F16>(a, batch, policy, s);
   }
-  return bf16 ? launch_decode<128, Bf16>(a, batch, reuse_kv, s)
-              : launch_decode<128, F16>(a, batch, reuse_kv, s);
+  return bf16 ? launch_decode<128, Bf16>(a, batch, policy, s)
+              : launch_decode<128, F16>(a, batch, policy, s);
 }
 
 }  // namespace

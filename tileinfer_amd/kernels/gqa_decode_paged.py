@@ -97,6 +97,13 @@ def _static_i32(values: tuple, dev: torch.device) -> torch.Tensor:
     return t
 
 
+def _policy_flag(kv_reuse: bool | None) -> int:
+    """Variant flag of the K/V cache policy: none (chosen on the device) for None."""
+    if kv_reuse is None:
+        return 0
+    return _lib.TI_DECODE_REUSE_KV if kv_reuse else _lib.TI_DECODE_STREAM_KV
+
+
 def _aligned_rows(t: torch.Tensor) -> bool:
     return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
             and all(s % 8 == 0 for s in t.stride()[:-1]))
@@ -162,7 +169,7 @@ def gqa_decode_paged_fn(
     out: torch.Tensor | None = None,
     split_tokens: int | None = None,
     variant: str = "auto",
-    kv_reuse: bool = False,
+    kv_reuse: bool | None = None,
     gate: torch.Tensor | None = None,
     shared_prefix_tokens: int = 0,
     prefix_pass: str = "auto",
@@ -179,10 +186,14 @@ def gqa_decode_paged_fn(
         out: keyword-only preallocated [B, H_q, D] output (contiguous, q's dtype)
         split_tokens: keyword-only split-K partition length (None: the library's choice)
         variant: keyword-only "auto" | "mfma" | "scalar" kernel choice
-        kv_reuse: keyword-only; True when the block tables share pages across sequences (prefix
-            caching), so K/V keeps the default cache policy and shared pages hit in L2/MALL; the
-            default streams every page once (``nt``), which is faster when nothing is shared.
-            Results are bitwise identical either way.
+        kv_reuse: keyword-only cache policy of the K/V loads. None (the default): chosen per
+            sequence on the device -- a sequence whose first block another sequence of the batch
+            also starts with (prefix caching shares block chains from the table's first column)
+            keeps the default policy, so the shared pages hit in L2/MALL for the other readers;
+            every other sequence streams its pages once (``nt``), which is faster when nothing is
+            shared (batches above 2,048 sequences stream). True forces the default policy, False
+            forces streaming. The scalar variant streams unless True. Results are bitwise
+            identical under every policy.
         gate: keyword-only; the attention output gate (model/qwen_36.py:1083), any tensor of
             B * H_q * D values laid out [B, H_q, D] (``q_gate`` [B, 1, H_q * D] as the model has
             it): the output is ``decode * sigmoid(gate)``, applied in the kernel's epilogue —
@@ -259,7 +270,7 @@ def gqa_decode_paged_fn(
             seqlen_kv.data_ptr(), out.data_ptr(), ws.data_ptr() if ws is not None else None,
             ws_bytes, b, h_q, h_kv, d, page_size, rows // page_size,
             table_width if prefix else width, int(split_tokens or 0),
-            _VARIANTS[variant] | (_lib.TI_DECODE_REUSE_KV if kv_reuse else 0), code)
+            _VARIANTS[variant] | _policy_flag(kv_reuse), code)
     g3 = None
     if gate is not None:
         if gate.numel() != b * h_q * d or gate.dtype != dt or gate.device != dev:
@@ -298,7 +309,7 @@ def gqa_decode_paged_noalloc(
     out: torch.Tensor,
     split_tokens: int | None = None,
     variant: str = "auto",
-    kv_reuse: bool = False,
+    kv_reuse: bool | None = None,
 ) -> torch.Tensor:
     """``gqa_decode_paged_fn`` for callers that cannot allocate: no output, workspace or copy is
     made (``ti_gqa_decode_paged_noalloc``; the split-K partials live in the library's per-GPU
@@ -320,6 +331,6 @@ def gqa_decode_paged_noalloc(
         q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
         block_table.data_ptr(), block_table.stride(0) if width > 0 else 0, seqlen_kv.data_ptr(),
         out.data_ptr(), b, h_q, h_kv, d, page_size, rows // page_size, width,
-        int(split_tokens or 0), _VARIANTS[variant] | (_lib.TI_DECODE_REUSE_KV if kv_reuse else 0),
+        int(split_tokens or 0), _VARIANTS[variant] | _policy_flag(kv_reuse),
         code, _lib.stream_handle(dev)))
     return out
