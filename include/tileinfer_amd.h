@@ -109,7 +109,9 @@ int ti_gqa_decode_plan(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
  * Replaces: gqa_decode_paged_fn(q, k_cache, v_cache, block_table, seqlen_kv, page_size=16)
  *           kernels/gqa_decode_paged.py:392-437 (math: ref_gqa_decode_paged, 444-461).
  *   q            [batch, num_q_heads, head_dim], last dim contiguous, strides q_stride_b/_h
- *   k/v_cache    [num_blocks, page_size, num_kv_heads, head_dim] contiguous (one layer's slab)
+ *   k/v_cache    [num_blocks, page_size, num_kv_heads, head_dim] contiguous (one layer's slab);
+ *                page_size 1, 2, 4, 8 or a multiple of 16 (the reference takes pages that divide
+ *                its 64-token tile, kernels/gqa_decode_paged.py:57-62, 408; engine/config.py:20)
  *   block_table  [batch, >= ceil(max seqlen / page_size)] int32, row stride block_table_stride;
  *                max_blocks_per_seq bounds every seqlen: seqlen[b] <= max_blocks_per_seq*page_size
  *   seqlen       [batch] int32 (the reference's seqlen_kv / context_lens)
@@ -173,7 +175,7 @@ int ti_copy_blocks(const void* src, void* dst, const int64_t* block_pairs, int64
  *                gives every CU the same number of key tiles (units cut between workgroups are
  *                merged in a fixed order; deterministic, but not batch-invariant); three launches
  *                (schedule, attention, merge). The workspace is scratch of this call only.
- * Launches on `stream`. head_dim 128 or 256; page_size a multiple of 16.
+ * Launches on `stream`. head_dim 128 or 256; page_size 4, 8 or a multiple of 16.
  */
 int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                          const void* k_cache, const void* v_cache, const int32_t* block_table,

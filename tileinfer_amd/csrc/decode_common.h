@@ -8,6 +8,9 @@
 namespace ti {
 
 constexpr int kMaxSplitPages = 1024;  // block ids of one partition staged in LDS
+// The MFMA kernel's balanced runs over pages smaller than its 16-token tile stage up to this
+// many block ids (8,192 tokens at page 2, 16,384 at page 4: one round of runs at config 3).
+constexpr int kMaxRunPagesSmall = 4096;
 constexpr int kMaxSplitTokens = 16384;
 
 struct Bf16 {};
@@ -120,6 +123,7 @@ struct DecodeArgs {
   int32_t* seq_first_tile;
   int32_t num_blocks32;  // block ids in [0, num_blocks32) are valid (int32 ids)
   int32_t hq, hkv, group, page_size, max_blocks, max_splits, split_tokens;
+  int32_t page_log2;  // log2(page_size) when it is a power of two (the small-page path)
   float scale_log2;
   // Balanced mode (> 0): this many workgroups share the batch's 16-token tiles evenly (every
   // workgroup takes a contiguous run of the concatenated tiles of all sequences); partials are

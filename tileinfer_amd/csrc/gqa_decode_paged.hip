@@ -27,6 +27,7 @@
 // Every O^T accumulator's head is its lane's head, so the softmax rescale needs no cross-lane
 // traffic; only the running max crosses the 4 lanes that share a head.
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "decode_common.h"
@@ -52,8 +53,13 @@ template <int D>
 struct Tile {
   u32x4 k[D / 32];      // [k-step]: row n, d in [32kk+8g, +8)
   u32x4 v[4][D / 128];  // [row 4g+r][chunk c]: d in [128c+8n, +8)
-  int rows;             // tokens of the tile that exist (uniform)
+  // Tokens of the tile that exist (uniform): pages of 16 tokens or more, a count of leading rows;
+  // smaller pages, a mask (bit t: row t is in the partition and its page's block id is valid).
+  int rows;
 };
+
+// Zeros that the small-page loads of absent rows read instead (one head's row, 512 bytes).
+__device__ __align__(16) uint16_t g_zero_row[256] = {};
 
 // Issues one tile's K and V loads (MFMA operand layout) with cache policy P.
 template <int D, int P>
@@ -120,14 +126,19 @@ __device__ __forceinline__ int balanced_chunk(const DecodeArgs& a, int total_til
   return max(per, a.chunk_min_tiles);
 }
 
-template <int D, typename Tag, int WPB, int POL>
+// SMALL: pages of 1, 2, 4 or 8 tokens (a 16-token tile spans 16 / page_size pages, so each lane
+// addresses its own rows' pages with a 64-bit address); otherwise pages of a multiple of 16
+// tokens (a tile lies in one page: one buffer descriptor per tile).
+template <int D, typename Tag, int WPB, int POL, bool SMALL>
 __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int batch) {
   constexpr int KK = D / 32;
   constexpr int NC = D / 128;
   constexpr int NT = D / 16;
   static_assert(D % 128 == 0, "head_dim must be a multiple of 128");
 
-  __shared__ int s_bids[kMaxSplitPages];
+  // Block ids of the current partition: pages smaller than a tile take more slots per token.
+  constexpr int kBidSlots = SMALL ? kMaxRunPagesSmall : kMaxSplitPages;
+  __shared__ int s_bids[kBidSlots];
   __shared__ int s_part[WPB + 4];
 
   const int lane = threadIdx.x & 63;
@@ -214,8 +225,48 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
   // compiler's count of outstanding loads exact, so waiting for one tile never waits for the tile
   // prefetched behind it.
   auto load_tile = [&](Tile<D>& T, int p) {
+    if constexpr (SMALL) {
+      // tok0 and p are multiples of 16, hence of the page size: the tile's pages are the
+      // partition's slots [slot0, slot0 + 16 / page_size).
+      const int L = a.page_log2;
+      const int slot0 = (p - tok0) >> L;
+      const int nrows = max(min(tok1 - p, 16), 0);
+      int mask = 0;
+      for (int j = 0; j < (16 >> L); ++j) {  // uniform
+        const int id = __builtin_amdgcn_readfirstlane(s_bids[min(slot0 + j, kBidSlots - 1)]);
+        if (uint32_t(id) < uint32_t(a.num_blocks32)) mask |= ((1 << a.page_size) - 1) << (j << L);
+      }
+      mask &= (1 << nrows) - 1;
+      // The address of one of this lane's rows (t), or of the zero row when t is absent.
+      auto row_ptr = [&](const uint16_t* cache, int t, int col) -> const uint16_t* {
+        if (!((mask >> t) & 1)) return g_zero_row + col;
+        const int id = s_bids[min(slot0 + (t >> L), kBidSlots - 1)];
+        return cache + int64_t(id) * a.page_stride + int64_t(t & (a.page_size - 1)) * a.row_stride +
+               kvh * D + col;
+      };
+      auto issue = [&](auto pol) {
+        constexpr int P = decltype(pol)::value;
+        const uint16_t* kp = row_ptr(a.k_cache, n, 8 * g);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) T.k[kk] = load16_policy<P>(kp + 32 * kk);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint16_t* vp = row_ptr(a.v_cache, 4 * g + r, 8 * n);
+#pragma unroll
+          for (int c = 0; c < NC; ++c) T.v[r][c] = load16_policy<P>(vp + 128 * c);
+        }
+      };
+      if constexpr (POL == kPolicyAuto) {
+        if (keep) issue(std::integral_constant<int, kPolicyKeep>{});
+        else issue(std::integral_constant<int, kPolicyStream>{});
+      } else {
+        issue(std::integral_constant<int, POL>{});
+      }
+      T.rows = mask;
+      return;
+    }
     // Past the partition end the LDS entry may be stale; `rows` is 0 there and masks it.
-    const int slot = min(p / a.page_size - tok0 / a.page_size, kMaxSplitPages - 1);
+    const int slot = min(p / a.page_size - tok0 / a.page_size, kBidSlots - 1);
     const int id = __builtin_amdgcn_readfirstlane(s_bids[slot]);
     const bool ok = (tok1 - p > 0) && (uint32_t(id) < uint32_t(a.num_blocks32));
     const int rows = ok ? min(tok1 - p, 16) : 0;
@@ -240,7 +291,10 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     for (int kk = 0; kk < KK; ++kk) s = mfma16x16x32(T.k[kk], qop[kk], s, Tag{});
     float sv[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sv[r] = (4 * g + r < T.rows) ? s[r] * a.scale_log2 : -INFINITY;
+    for (int r = 0; r < 4; ++r) {
+      const bool present = SMALL ? ((T.rows >> (4 * g + r)) & 1) != 0 : 4 * g + r < T.rows;
+      sv[r] = present ? s[r] * a.scale_log2 : -INFINITY;
+    }
     float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -296,8 +350,8 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
       }
     }
     const int page0 = tok0 / a.page_size;
-    // The plan keeps every partition within kMaxSplitPages pages; the clamp only guards LDS.
-    const int npages = tok1 > tok0 ? min((tok1 - 1) / a.page_size - page0 + 1, kMaxSplitPages) : 0;
+    // The plan keeps every partition within kBidSlots pages; the clamp only guards LDS.
+    const int npages = tok1 > tok0 ? min((tok1 - 1) / a.page_size - page0 + 1, kBidSlots) : 0;
     // The sequence's first block id (cache policy), requested with the partition's block ids.
     const int first_id =
         (POL == kPolicyAuto && share_slots > 0 && npages > 0) ? a.block_table[b * a.bt_stride] : -1;
@@ -831,20 +885,26 @@ __global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int 
   for (int j = 0; j < PER; j += 2) put(j, pack2(acc[j] * inv, acc[j + 1] * inv, Tag{}));
 }
 
-template <int D, typename Tag, int WPB>
-int launch_mfma(const DecodeArgs& a, int batch, int policy, hipStream_t stream) {
+template <int D, typename Tag, int WPB, bool SMALL>
+void launch_mfma_pages(const DecodeArgs& a, int batch, int policy, hipStream_t stream) {
   const dim3 grid = a.balanced_wgs > 0 ? dim3(a.hkv / WPB, a.balanced_wgs, 1)
                                         : dim3(a.hkv / WPB, a.max_splits, batch);
   if (policy == kPolicyKeep) {
-    hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyKeep>), grid, dim3(64 * WPB), 0,
-                       stream, a, batch);
+    hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyKeep, SMALL>), grid, dim3(64 * WPB),
+                       0, stream, a, batch);
   } else if (policy == kPolicyStream) {
-    hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyStream>), grid, dim3(64 * WPB), 0,
-                       stream, a, batch);
+    hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyStream, SMALL>), grid,
+                       dim3(64 * WPB), 0, stream, a, batch);
   } else {
-    hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyAuto>), grid, dim3(64 * WPB), 0,
-                       stream, a, batch);
+    hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, WPB, kPolicyAuto, SMALL>), grid, dim3(64 * WPB),
+                       0, stream, a, batch);
   }
+}
+
+template <int D, typename Tag, int WPB>
+int launch_mfma(const DecodeArgs& a, int batch, int policy, hipStream_t stream) {
+  if (a.page_size < 16) launch_mfma_pages<D, Tag, WPB, true>(a, batch, policy, stream);
+  else launch_mfma_pages<D, Tag, WPB, false>(a, batch, policy, stream);
   return check_launch("ti_gqa_decode_paged (mfma)");
 }
 
@@ -909,8 +969,9 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
   if (D != 128 && D != 256) {
     return fail(TI_EUNSUPPORTED, "decode: head_dim %d not built (128, 256)", D);
   }
-  if (page_size <= 0 || page_size % 16 != 0) {
-    return fail(TI_EUNSUPPORTED, "decode: page_size %d is not a positive multiple of 16",
+  if (page_size <= 0 || (page_size % 16 != 0 && 16 % page_size != 0)) {
+    return fail(TI_EUNSUPPORTED,
+                "decode: page_size %d is neither 1, 2, 4, 8 nor a positive multiple of 16",
                 page_size);
   }
   if (max_blocks < 0) return fail(TI_EINVAL, "decode: max_blocks_per_seq %d < 0", max_blocks);
@@ -954,7 +1015,9 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
     // contexts: shorter runs pay more start-ups.) When runs that long would exceed the block ids
     // one workgroup stages in LDS (a run may start mid-page: one page of slack), whole further
     // rounds: a partial last round would run alone after the others and nearly double the time.
-    const int64_t max_chunk = int64_t(kMaxSplitPages - 1) * (page_size / 16);
+    // (Pages smaller than a tile: runs start on a tile, hence on a page, so no slack page.)
+    const int64_t max_chunk = page_size >= 16 ? int64_t(kMaxSplitPages - 1) * (page_size / 16)
+                                              : int64_t(kMaxRunPagesSmall) / (16 / page_size);
     const int64_t bound_tiles = ceil_div(bound, 16);
     const int64_t per_round = cus * 4 / hkv > 0 ? cus * 4 / hkv : 1;
     const int64_t needed = ceil_div(int64_t(batch) * bound_tiles, max_chunk);
@@ -1085,6 +1148,8 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
   a.hkv = num_kv_heads;
   a.group = num_q_heads / num_kv_heads;
   a.page_size = page_size;
+  a.page_log2 = 0;
+  while ((1 << a.page_log2) < page_size && a.page_log2 < 30) ++a.page_log2;
   a.max_blocks = max_blocks_per_seq;
   a.max_splits = max_splits;
   a.split_tokens = split;

@@ -24,6 +24,7 @@
 //   O^T[16 d x 16 rows]    += V^T[16 d x 32 keys] . P^T[32 keys x 16 rows]   (16x16x32)
 // so each accumulator's query row is its lane's column and the softmax stays inside the lane.
 #include <atomic>
+#include <type_traits>
 
 #include "decode_common.h"
 
@@ -311,7 +312,10 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs 
 // reads are free of bank conflicts.
 // P2: page_size is a power of two (page_shift >= 0); pages are then found with shifts (a runtime
 // division costs ~20 scalar instructions, several per tile).
-template <int D, int C, int W, int NS, bool P2, typename Tag>
+// SMALL: pages of 4 or 8 tokens (P2 as well). A 16-key sub-tile then spans 16 / page_size pages:
+// each 1 KiB load (2 or 4 rows) lies in one page and gets that page's descriptor, and the keys
+// present in a stage are a bit mask (an absent page can share a sub-tile with a present one).
+template <int D, int C, int W, int NS, bool P2, bool SMALL, typename Tag>
 __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int kKT = 16 * NS;
   constexpr int KK = D / 32;
@@ -400,9 +404,39 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   // The ids are read with scalar loads: a vector load would be counted with the K/V loads into
   // LDS, and waiting for the ids (used right away) would then wait for the whole tile in flight.
   int nbid[NS];
+  // SMALL: the next tile's present keys (bit 16 j + i: key i of sub-tile j is inside the context
+  // and its page valid) and the block ids of the pages of this wave's sub-tile (-1: absent).
+  uint64_t nmask = 0;
+  int nsid0 = -1, nsid1 = -1, nsid2 = -1, nsid3 = -1;  // scalars: an array would go to LDS
   auto load_ids = [&](int k0) __attribute__((always_inline)) {
     typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
     const const_i32_ptr row = (const_i32_ptr)bt_row;
+    if constexpr (SMALL) {
+      const int ps = a.page_size;
+      uint64_t mask = 0;
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+#pragma unroll
+        for (int pj = 0; pj < 4; ++pj) {
+          const int key0 = k0 + 16 * j + pj * ps;
+          if (pj * ps < 16) {  // uniform
+            const int id = key0 < sx.kv_len ? row[key0 >> a.page_shift] : -1;
+            const bool ok = uint32_t(id) < uint32_t(a.num_blocks32);
+            if (ok) mask |= uint64_t((1u << ps) - 1u) << (16 * j + pj * ps);
+            if (j == my_sub) {
+              const int v = ok ? id : -1;
+              if (pj == 0) nsid0 = v;
+              else if (pj == 1) nsid1 = v;
+              else if (pj == 2) nsid2 = v;
+              else nsid3 = v;
+            }
+          }
+        }
+      }
+      const int live = min(max(sx.kv_len - k0, 0), 16 * NS);  // keys inside the context
+      nmask = live >= 64 ? mask : mask & ((uint64_t(1) << live) - 1);
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       const int key0 = k0 + 16 * j;
@@ -415,13 +449,54 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     return min(max(sx.kv_len - key0, 0), 16);
   };
   // Sub-tiles of each stage with nothing loaded (bit j; uniform). Kept as two masks rather than
-  // per-sub-tile row counts: the tile loop is short of scalar registers.
-  uint32_t empty_st[2];
+  // per-sub-tile row counts: the tile loop is short of scalar registers. SMALL: the stage's
+  // present keys instead (bit 16 j + i).
+  typedef std::conditional_t<SMALL, uint64_t, uint32_t> StageMask;
+  StageMask empty_st[2];
   // Issue this wave's loads of the tile at key k0 into stage (sk, sv). A sub-tile lies in one
   // page; its loads use a buffer descriptor spanning only the rows that exist, so rows past the
   // context or in an absent page land in LDS as zero without a memory access.
-  auto fetch = [&](uint16_t* sk, uint16_t* sv, uint32_t& empty_out, int k0)
+  auto fetch = [&](uint16_t* sk, uint16_t* sv, StageMask& empty_out, int k0)
       __attribute__((always_inline)) {
+    if constexpr (SMALL) {
+      empty_out = nmask;
+      if (wave >= LW) return;  // uniform: the other waves only need the mask
+      const int ps = a.page_size;
+      const int key_sub = k0 + 16 * my_sub;
+      const int q = lane / CPR;
+      const int slot = lane % CPR;
+      int wblk = wave * LPW;
+      asm volatile("" : "+s"(wblk));
+      const int bw = (wblk * RPB) & 15;
+      const uint32_t lane_hi = __umul24(uint32_t(bw | q), row_bytes);
+      const uint32_t lane_k = uint32_t(slot ^ lds_swizzle(bw | q)) * 16u;
+      const uint32_t lane_v = uint32_t(slot ^ lds_swizzle_v(bw | q)) * 16u;
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) {
+        const int blk = wblk + i;                  // 1 KiB block of the tile (uniform)
+        const int rb = bw + RPB * i;               // its first row in the sub-tile
+        const int pj = rb >> a.page_shift;         // its page in the sub-tile (ps >= RPB)
+        const int id = pj == 0 ? nsid0 : pj == 1 ? nsid1 : pj == 2 ? nsid2 : nsid3;
+        const int present = id < 0 ? 0 : min(max(sx.kv_len - (key_sub + pj * ps), 0), ps);
+        const uint32_t nbytes = present > 0 ? uint32_t(present - 1) * row_bytes + D * 2 : 0u;
+        const int64_t base = int64_t(id < 0 ? 0 : id) * a.page_stride + int64_t(kvh) * D;
+        // Offsets as the page-16 form computes them (relative to the sub-tile), moved to the
+        // page's first row.
+        const uint32_t ri = uint32_t(RPB * i) * row_bytes - uint32_t(pj * ps) * row_bytes;
+        const uint32_t off_k = ((lane_k ^ uint32_t(16 * lds_swizzle(RPB * i))) + lane_hi) + ri;
+        const uint32_t off_v = ((lane_v ^ uint32_t(16 * lds_swizzle_v(RPB * i))) + lane_hi) + ri;
+        if constexpr (kAsmLoads) {
+          load_lds16(rsrc_words(a.k_cache + base, nbytes), off_k, sk + blk * 512);
+          load_lds16(rsrc_words(a.v_cache + base, nbytes), off_v, sv + blk * 512);
+        } else {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.k_cache + base, nbytes),
+                                                   (lds_ptr_t)(sk + blk * 512), 16, off_k, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.v_cache + base, nbytes),
+                                                   (lds_ptr_t)(sv + blk * 512), 16, off_v, 0, 0, 0);
+        }
+      }
+      return;
+    }
     int bid = nbid[0];
     uint32_t empty = nbid[0] < 0 ? 1u : 0u;
 #pragma unroll
@@ -492,7 +567,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   };
 
   // Q.K^T of the tile at k0 (stage sk), the online softmax, and P^T in MFMA operand form.
-  auto qk_softmax = [&](const uint16_t* sk, uint32_t empty, int k0, u32x4 (&pop)[C][NS / 2])
+  auto qk_softmax = [&](const uint16_t* sk, StageMask empty, int k0, u32x4 (&pop)[C][NS / 2])
       __attribute__((always_inline)) {
     // S^T of each sub-tile that holds a key some row of the wave can see; the rest stay zero.
     f32x4 s[NS][C];
@@ -503,7 +578,11 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       for (int c = 0; c < C; ++c) s[j][c] = f32x4{0.f, 0.f, 0.f, 0.f};
       rows[j] = 0;
       if (k0 + 16 * j <= wave_last_key) {  // uniform
-        rows[j] = ((empty >> j) & 1u) ? 0 : sub_rows(k0 + 16 * j);
+        if constexpr (SMALL) {
+          rows[j] = int((empty >> (16 * j)) & 0xffffu);  // present keys of the sub-tile
+        } else {
+          rows[j] = ((empty >> j) & 1u) ? 0 : sub_rows(k0 + 16 * j);
+        }
         auto read_k = [&](int kk) __attribute__((always_inline)) {
           return *reinterpret_cast<const u32x4*>(sk + (16 * j + n) * D +
                                                 (((4 * kk + g) ^ lds_swizzle(n)) * 8));
@@ -538,7 +617,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     // A tile wholly below the wave's diagonal with every key present needs no mask (uniform).
     bool full = k0 + kKT - 1 <= wave_first_key;
 #pragma unroll
-    for (int j = 0; j < NS; ++j) full = full && rows[j] == 16;
+    for (int j = 0; j < NS; ++j) full = full && rows[j] == (SMALL ? 0xffff : 16);
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       float v[4 * NS];
@@ -554,7 +633,8 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int i0 = 4 * g + r;
-            const bool ok = row_ok[c] & (i0 < rows[j]) & (k0 + 16 * j + i0 <= q_pos[c]);
+            const bool present = SMALL ? ((rows[j] >> i0) & 1) != 0 : i0 < rows[j];
+            const bool ok = row_ok[c] & present & (k0 + 16 * j + i0 <= q_pos[c]);
             v[4 * j + r] = ok ? s[j][c][r] : -INFINITY;
           }
         }
@@ -636,7 +716,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     }
   };
 
-  auto compute = [&](const uint16_t* sk, const uint16_t* sv, uint32_t empty, int k0)
+  auto compute = [&](const uint16_t* sk, const uint16_t* sv, StageMask empty, int k0)
       __attribute__((always_inline)) {
     u32x4 pop[C][NS / 2];
     qk_softmax(sk, empty, k0, pop);
@@ -1003,10 +1083,10 @@ int prefill_key_tile(int head_dim, bool balanced) {
   return head_dim == 256 && balanced ? 16 * 2 : 16 * 4;
 }
 
-template <int D, bool BAL, bool P2, typename Tag>
+template <int D, bool BAL, bool P2, typename Tag, bool SMALL = false>
 constexpr auto prefill_kernel() {
   using S = PrefillShape<D, BAL>;
-  return prefill_mfma_kernel<D, S::C, S::W, S::NS, P2, Tag>;
+  return prefill_mfma_kernel<D, S::C, S::W, S::NS, P2, SMALL, Tag>;
 }
 
 // Workgroups of one balanced launch: every CU's resident workgroups (one round).
@@ -1037,8 +1117,9 @@ int balanced_wgs_bound(int head_dim) {
 template <int D, bool BAL, typename Tag>
 int launch_prefill(const PrefillArgs& a, int batch, int max_q, hipStream_t s) {
   using S = PrefillShape<D, BAL>;
-  const auto kern = a.page_shift >= 0 ? prefill_kernel<D, BAL, true, Tag>()
-                                      : prefill_kernel<D, BAL, false, Tag>();
+  const auto kern = a.page_size < 16   ? prefill_kernel<D, BAL, true, Tag, true>()
+                    : a.page_shift >= 0 ? prefill_kernel<D, BAL, true, Tag>()
+                                        : prefill_kernel<D, BAL, false, Tag>();
   if constexpr (!BAL) {
     const dim3 grid(unsigned(a.hkv), unsigned(ceil_div(int64_t(max_q) * a.group, S::C * S::W * 16)),
                     unsigned(batch * a.key_splits));
@@ -1136,8 +1217,9 @@ int prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h, const v
     return fail(TI_EUNSUPPORTED, "ti_gqa_prefill_paged: head_dim %d not built (128, 256)",
                 head_dim);
   }
-  if (page_size <= 0 || page_size % 16 != 0) {
-    return fail(TI_EUNSUPPORTED, "ti_gqa_prefill_paged: page_size %d not a multiple of 16",
+  if (page_size <= 0 || (page_size % 16 != 0 && page_size != 8 && page_size != 4)) {
+    return fail(TI_EUNSUPPORTED,
+                "ti_gqa_prefill_paged: page_size %d is neither 4, 8 nor a multiple of 16",
                 page_size);
   }
   if (key_splits < 1 || (key_splits > 1 && (workspace != nullptr || uo == nullptr)) ||

@@ -125,7 +125,7 @@ def gqa_prefill_paged_fn(
             ``cu_seqlens_k[b+1] - cu_seqlens_k[b]``, i.e. ``full_kv_len``)
         max_seqlen_q: host bound on every query length (the reference's ``max_seqlen_q``); None
             reads it from ``cu_seqlens_q`` (one device-to-host copy)
-        page_size: tokens per page of the flattened cache (a multiple of 16)
+        page_size: tokens per page of the flattened cache (4, 8 or a multiple of 16)
         causal: keyword-only; False drops the causal mask (the reference's ``is_causal=False``)
         out: keyword-only preallocated [total_q, H_q, D] output
         batch_invariant: keyword-only; forces the per-unit schedule (bitwise batch- and

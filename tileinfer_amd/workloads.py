@@ -67,9 +67,9 @@ def _randn(shape, gen, device, dtype, scale=1.0):
 
 
 def tables_from_pool(ctx: list[int], pool: int, gen: torch.Generator, device,
-                     width: int | None = None) -> torch.Tensor:
+                     width: int | None = None, page: int = BLOCK) -> torch.Tensor:
     """Disjoint random physical blocks per sequence, drawn from randperm(pool); -1 padded."""
-    need = [(c + BLOCK - 1) // BLOCK for c in ctx]
+    need = [(c + page - 1) // page for c in ctx]
     if sum(need) > pool:
         raise ValueError(f"pool {pool} < {sum(need)} blocks needed")
     perm = torch.randperm(pool, generator=gen, device=device).to(torch.int32)
@@ -82,29 +82,31 @@ def tables_from_pool(ctx: list[int], pool: int, gen: torch.Generator, device,
     return table
 
 
-def decode_slots(table: torch.Tensor, ctx: list[int]) -> torch.Tensor:
+def decode_slots(table: torch.Tensor, ctx: list[int], page: int = BLOCK) -> torch.Tensor:
     """Slot of the token at position ctx-1 of every sequence (-1 for an empty sequence)."""
     pos = torch.tensor([max(c - 1, 0) for c in ctx], dtype=torch.int64)
-    rows = table.cpu()[torch.arange(len(ctx)), pos // BLOCK].long()
-    slots = rows * BLOCK + pos % BLOCK
+    rows = table.cpu()[torch.arange(len(ctx)), pos // page].long()
+    slots = rows * page + pos % page
     slots[torch.tensor([c <= 0 for c in ctx], dtype=torch.bool)] = -1
     return slots.to(torch.int32).to(table.device)
 
 
 def make_step(ctx: list[int], pool: int, seed: int, device="cpu", dtype=torch.bfloat16,
               value_scale: float = 1.0, width: int | None = None, hq: int = HQ, hkv: int = HKV,
-              d: int = HEAD_DIM) -> PagedStep:
+              d: int = HEAD_DIM, page: int = BLOCK) -> PagedStep:
+    """Random tables over a pool of `pool` pages of `page` tokens ([pool, page, hkv, d] caches)."""
     gen = torch.Generator(device=device).manual_seed(seed)
-    table = tables_from_pool(ctx, pool, gen, device, width)
-    k_cache = _randn((pool, BLOCK, hkv, d), gen, device, dtype, value_scale)
-    v_cache = _randn((pool, BLOCK, hkv, d), gen, device, dtype, value_scale)
+    table = tables_from_pool(ctx, pool, gen, device, width, page)
+    k_cache = _randn((pool, page, hkv, d), gen, device, dtype, value_scale)
+    v_cache = _randn((pool, page, hkv, d), gen, device, dtype, value_scale)
     b = len(ctx)
     q = _randn((b, hq, d), gen, device, dtype, value_scale)
     k_new = _randn((b, hkv, d), gen, device, dtype, value_scale)
     v_new = _randn((b, hkv, d), gen, device, dtype, value_scale)
-    return PagedStep(q=q, k_new=k_new, v_new=v_new, slot_mapping=decode_slots(table, ctx),
+    return PagedStep(q=q, k_new=k_new, v_new=v_new, slot_mapping=decode_slots(table, ctx, page),
                      block_table=table, seqlen=torch.tensor(ctx, dtype=torch.int32, device=device),
-                     k_cache=k_cache, v_cache=v_cache, meta={"seed": seed, "ctx": list(ctx)})
+                     k_cache=k_cache, v_cache=v_cache, page_size=page,
+                     meta={"seed": seed, "ctx": list(ctx)})
 
 
 def config1(seed: int = 1001, device="cpu", ctx: int = 512) -> PagedStep:
@@ -304,16 +306,17 @@ def prefill_flops(q_lens: list[int], kv_lens: list[int], hq: int = HQ, d: int = 
 def prefill_step(q_lens: list[int], kv_lens: list[int], seed: int, device="cpu",
                  pool: int | None = None, dtype=torch.bfloat16, value_scale: float = 1.0,
                  hq: int = HQ, hkv: int = HKV, d: int = HEAD_DIM,
-                 width: int | None = None) -> PrefillStep:
-    """Random non-contiguous tables from a pool (1.25x the need by default), N(0,1)·scale values."""
+                 width: int | None = None, page: int = BLOCK) -> PrefillStep:
+    """Random non-contiguous tables from a pool (1.25x the need by default), N(0,1)·scale values;
+    pages of `page` tokens."""
     if len(q_lens) != len(kv_lens):
         raise ValueError("q_lens and kv_lens differ in length")
-    need = sum((c + BLOCK - 1) // BLOCK for c in kv_lens)
+    need = sum((c + page - 1) // page for c in kv_lens)
     pool = max(1, math.ceil(1.25 * need)) if pool is None else pool
     gen = torch.Generator(device=device).manual_seed(seed)
-    table = tables_from_pool(kv_lens, pool, gen, device, width)
-    k_cache = _randn((pool, BLOCK, hkv, d), gen, device, dtype, value_scale)
-    v_cache = _randn((pool, BLOCK, hkv, d), gen, device, dtype, value_scale)
+    table = tables_from_pool(kv_lens, pool, gen, device, width, page)
+    k_cache = _randn((pool, page, hkv, d), gen, device, dtype, value_scale)
+    v_cache = _randn((pool, page, hkv, d), gen, device, dtype, value_scale)
     cu = [0]
     for n in q_lens:
         cu.append(cu[-1] + n)
@@ -322,6 +325,7 @@ def prefill_step(q_lens: list[int], kv_lens: list[int], seed: int, device="cpu",
                        cu_seqlens_q=torch.tensor(cu, dtype=torch.int32, device=device),
                        seqlen_k=torch.tensor(kv_lens, dtype=torch.int32, device=device),
                        k_cache=k_cache, v_cache=v_cache, max_seqlen_q=max(q_lens, default=0),
+                       page_size=page,
                        meta={"seed": seed, "q_lens": list(q_lens), "kv_lens": list(kv_lens)})
 
 
