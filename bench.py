@@ -811,6 +811,9 @@ def main():
                     help="skip the append sizes, 2,048-token partitions and context sweep")
     ap.add_argument("--sequential-tables", action="store_true",
                     help="diagnostic: contiguous blocks per sequence instead of random permutations")
+    ap.add_argument("--page-size", type=int, default=BLOCK,
+                    help="config 3's decode through pages of 1, 2, 4 or 8 tokens viewing the same "
+                         "memory (the same tokens in the same 16-token tiles), default 16")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -835,8 +838,20 @@ def main():
                                                              args.sequential_tables)
     torch.cuda.synchronize()
     log(f"cache {kv.numel() * 2 / 2**30:.1f} GiB ready")
+    page = args.page_size
+    if page <= 0 or BLOCK % page:
+        raise SystemExit(f"--page-size {page}: choose 1, 2, 4, 8 or 16")
     views = [layer_views(kv, l) for l in range(layers)]
-    split, max_splits, ws = decode_plan(b, HQ, HKV, HEAD_DIM, BLOCK, tables[0].shape[1],
+    dec_tables = tables
+    if page != BLOCK:
+        # The same slab viewed as pages of `page` tokens: block i of a table becomes blocks
+        # r i .. r i + r - 1 (r = 16 / page), the same rows in the same order.
+        r = BLOCK // page
+        cols = torch.arange(tables[0].shape[1] * r, device=dev)
+        dec_tables = [(t[:, cols // r] * r + cols % r).to(torch.int32) for t in tables]
+        views = [(kr, vr, kp.view(-1, page, HKV, HEAD_DIM), vp.view(-1, page, HKV, HEAD_DIM))
+                 for kr, vr, kp, vp in views]
+    split, max_splits, ws = decode_plan(b, HQ, HKV, HEAD_DIM, page, dec_tables[0].shape[1],
                                         args.split_tokens)
 
     def step(ev=None):
@@ -848,7 +863,7 @@ def main():
             store_kvcache(k_new[l], v_new[l], k_rows, v_rows, slots[l])
             if ev is not None:
                 ev[l][1].record()
-            out = gqa_decode_paged_fn(q[l], k_paged, v_paged, tables[l], seqlen, BLOCK,
+            out = gqa_decode_paged_fn(q[l], k_paged, v_paged, dec_tables[l], seqlen, page,
                                       split_tokens=args.split_tokens, variant=args.variant)
             if ev is not None:
                 ev[l][2].record()
@@ -886,7 +901,7 @@ def main():
 
     ms_step = total_ms / args.steps
     a_bytes = append_bytes(slots[0], HKV * HEAD_DIM)
-    d_bytes = decode_bytes([ctx] * b)
+    d_bytes = decode_bytes([ctx] * b, page_size=page)
     step_bytes = layers * (a_bytes + d_bytes)
     dec_avg_us = statistics.mean(dec_ms) * 1e3
     app_avg_us = statistics.mean(app_ms) * 1e3
@@ -915,6 +930,7 @@ def main():
                           else f"fixed {split} tokens, up to {max_splits} per sequence"),
             "variant": args.variant,
             "tables": "sequential" if args.sequential_tables else "random permutation per layer",
+            "page_size": page,
         },
         "us_per_layer_step": round(ms_step * 1e3 / layers, 2),
         "decode_us_per_layer": round(dec_avg_us, 2),
@@ -945,7 +961,7 @@ def main():
         def fused_step():
             for l in range(layers):
                 _, _, k_paged, v_paged = views[l]
-                gqa_decode_paged_fn(q[l], k_paged, v_paged, tables[l], seqlen, BLOCK,
+                gqa_decode_paged_fn(q[l], k_paged, v_paged, dec_tables[l], seqlen, page,
                                     split_tokens=args.split_tokens, variant=args.variant,
                                     append=(k_new[l], v_new[l], slots[l]))
         two_ms, fused_ms = (t / 1e3 for t in _time_interleaved([step, fused_step], args.steps,
