@@ -119,11 +119,20 @@ __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
   return x;
 }
 
+// Batches of at most this many 16-token tiles in all take runs of kShortChunkTiles: there the
+// runs' one round of tile loads matters more than the merge's extra parts (graph-timed GPU time,
+// same box: config 1's 32 tiles 14.3 -> 12.6 us, 4 sequences of 67 tiles 18.4 -> 14.6, 2 of 76
+// 16.1 -> 14.7; one sequence of 128 tiles went 17.6 -> 18.4 with them, so it keeps 4).
+constexpr int kShortBatchTiles = 96;
+constexpr int kShortChunkTiles = 2;
+
 // Total 16-token tiles of the batch and the balanced run length (same in every workgroup and in
 // the merge: a pure function of the sequence lengths and the plan).
 __device__ __forceinline__ int balanced_chunk(const DecodeArgs& a, int total_tiles) {
   const int per = (total_tiles + a.balanced_wgs - 1) / a.balanced_wgs;
-  return max(per, a.chunk_min_tiles);
+  const int least = total_tiles <= kShortBatchTiles ? min(kShortChunkTiles, a.chunk_min_tiles)
+                                                    : a.chunk_min_tiles;
+  return max(per, least);
 }
 
 // SMALL: pages of 1, 2, 4 or 8 tokens (a 16-token tile spans 16 / page_size pages, so each lane
