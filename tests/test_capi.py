@@ -33,7 +33,7 @@ def test_header_codes_match_binding():
     text = HEADER.read_text()
     for name in ("TI_OK", "TI_EINVAL", "TI_ELAUNCH", "TI_EUNSUPPORTED", "TI_DTYPE_BF16",
                  "TI_DTYPE_F16", "TI_DECODE_AUTO", "TI_DECODE_MFMA", "TI_DECODE_SCALAR",
-                 "TI_DECODE_REUSE_KV"):
+                 "TI_DECODE_REUSE_KV", "TI_DECODE_STREAM_KV"):
         m = re.search(rf"#define {name} (0x[0-9a-fA-F]+|\d+)", text)
         assert m and int(m.group(1), 0) == getattr(_lib, name), name
 
@@ -71,7 +71,10 @@ def test_balanced_plan_one_wave_per_simd_in_whole_rounds():
 
 
 @pytest.mark.parametrize("args,code", [
-    ((4, 24, 4, 256, 8, 100, 2048), _lib.TI_EUNSUPPORTED),    # page size not a multiple of 16
+    ((4, 24, 4, 256, 12, 100, 2048), _lib.TI_EUNSUPPORTED),   # page neither 1/2/4/8 nor 16k
+    ((4, 24, 4, 256, 24, 100, 2048), _lib.TI_EUNSUPPORTED),   # 24: not a multiple of 16
+    ((4, 24, 4, 256, 0, 100, 2048), _lib.TI_EUNSUPPORTED),    # no page size
+    ((4, 24, 4, 256, 8, 100, 48), _lib.TI_EINVAL),            # split not a multiple of 32
     ((4, 64, 2, 256, 16, 100, 2048), _lib.TI_EUNSUPPORTED),   # group of 32 > 16-row tile
     ((4, 24, 4, 96, 16, 100, 2048), _lib.TI_EUNSUPPORTED),    # head_dim not built
     ((4, 24, 4, 256, 16, 100, 100), _lib.TI_EINVAL),          # split not a multiple of 32
@@ -82,6 +85,49 @@ def test_decode_plan_rejects(args, code):
     rc = _plan(*args)[0]
     assert rc == code
     assert _lib.load().ti_last_error().decode()
+
+
+def test_decode_plan_small_pages():
+    """Pages of 1, 2, 4 and 8 tokens plan like 16-token pages of the same context: the kernel
+    still walks 16-token tiles, so the balanced plan's workgroup count does not change; a split
+    is a multiple of 32 tokens whatever the page size."""
+    for ps in (1, 2, 4, 8):
+        rc, split, wgs, ws = _plan(64, 24, 4, 256, ps, 8192 * 16 // ps // 16, 0)
+        assert rc == _lib.TI_OK, ps
+        assert (split, wgs) == (0, 256)
+        rc, split, ms, _ = _plan(8, 24, 4, 256, ps, 2048 // ps, 512)
+        assert (rc, split, ms) == (_lib.TI_OK, 512, 4)
+
+
+def _decode_abi(variant, batch=0):
+    lib = _lib.load()
+    return lib.ti_gqa_decode_paged(None, 0, 0, None, None, None, 8, None, None, None, 0, batch,
+                                   24, 4, 256, 16, 16, 8, 0, variant, _lib.TI_DTYPE_BF16, None)
+
+
+def test_decode_cache_policy_flags():
+    """The two cache-policy flags: each alone is accepted (an empty batch is then a no-op), both
+    together are refused before the plan, as is an unknown flag bit."""
+    lib = _lib.load()
+    for v in (0, _lib.TI_DECODE_REUSE_KV, _lib.TI_DECODE_STREAM_KV,
+              _lib.TI_DECODE_MFMA | _lib.TI_DECODE_STREAM_KV,
+              _lib.TI_DECODE_SCALAR | _lib.TI_DECODE_REUSE_KV):
+        assert _decode_abi(v) == _lib.TI_OK, hex(v)
+    for v in (_lib.TI_DECODE_REUSE_KV | _lib.TI_DECODE_STREAM_KV, 0x40, 3):
+        assert _decode_abi(v) == _lib.TI_EINVAL, hex(v)
+        assert b"variant" in lib.ti_last_error()
+    # A non-empty batch with a valid flag gets as far as the null operands.
+    assert _decode_abi(_lib.TI_DECODE_STREAM_KV, batch=2) == _lib.TI_EINVAL
+    assert b"null" in lib.ti_last_error()
+
+
+def test_policy_flag_from_kv_reuse():
+    """The Python keyword maps onto the flags: None leaves the choice to the device, True keeps
+    K/V cacheable, False streams them."""
+    from tileinfer_amd.kernels.gqa_decode_paged import _policy_flag
+    assert _policy_flag(None) == 0
+    assert _policy_flag(True) == _lib.TI_DECODE_REUSE_KV
+    assert _policy_flag(False) == _lib.TI_DECODE_STREAM_KV
 
 
 def test_append_argument_errors_without_device():
@@ -154,7 +200,10 @@ def test_prefill_argument_errors_without_device():
     assert _prefill_abi(total_q=0) == _lib.TI_OK
     assert _prefill_abi(dtype=7) == _lib.TI_EUNSUPPORTED
     assert _prefill_abi(d=96) == _lib.TI_EUNSUPPORTED
-    assert _prefill_abi(ps=8) == _lib.TI_EUNSUPPORTED
+    for ps in (1, 2, 12, 24):                       # 4, 8 and multiples of 16 are built
+        assert _prefill_abi(ps=ps) == _lib.TI_EUNSUPPORTED, ps
+    for ps in (4, 8, 32):                           # accepted: fails later, on the null operands
+        assert _prefill_abi(ps=ps) == _lib.TI_EINVAL, ps
     assert _prefill_abi(hq=25) == _lib.TI_EINVAL
     rc = _prefill_abi()
     assert rc == _lib.TI_EINVAL and b"null" in _lib.load().ti_last_error()

@@ -397,6 +397,34 @@ def test_block_ids_outside_the_pool_are_refused():
     assert bm.ref_counts.tolist() == [1, 0, 0, 0] and bm.num_free_blocks == 3
 
 
+def test_config5_managed_builder_shares_the_prefix_and_swaps_private_blocks():
+    """The managed config-5 set-up at a small size on the CPU: every sequence's table starts with
+    the same physical prefix blocks (refcount = batch), the pool holds exactly the physical blocks,
+    the shared-prefix length is the whole prefix, and swapping out a quarter of the sequences moves
+    only their private blocks into the host pool, which then holds exactly those."""
+    from tileinfer_amd.workloads import config5_managed
+    batch, prefix, suffix = 8, 256, 64
+    mb = config5_managed(device="cpu", layers=2, batch=batch, prefix=prefix, suffix=suffix)
+    m, pb, sb = mb.manager, prefix // 16, suffix // 16
+    table, seqlen = mb.tables()
+    assert table.shape == (batch, pb + sb) and seqlen.tolist() == [prefix + suffix] * batch
+    assert bool((table[:, :pb] == table[0, :pb]).all())
+    private = table[:, pb:].flatten().tolist()
+    assert len(set(private)) == batch * sb and not set(private) & set(table[0, :pb].tolist())
+    bm = m.block_manager
+    assert bm.num_free_blocks == 0 and mb.kv.shape[2] == pb + batch * sb
+    assert all(int(bm.ref_counts[b]) == batch for b in table[0, :pb].tolist())
+    assert m.common_prefix_tokens(mb.seqs) == prefix
+    assert mb.q.shape == (2, batch, 24, 256)
+    victims = mb.seqs[:batch // 4]
+    pairs = [p for s in victims for p in m.swap_out(s)]
+    assert sorted(d for d, _ in pairs) == sorted(table[:batch // 4, pb:].flatten().tolist())
+    assert m.host_free == [] and bm.num_free_blocks == len(pairs)
+    for s in victims:
+        assert s.block_table[:pb] == table[0, :pb].tolist() and s.block_table[pb:] == [-1] * sb
+        assert m.can_swap_in(s) and len(m.swap_in(s)) == sb
+
+
 # ----------------------------------------------------------------------------- prefix index: races
 
 
