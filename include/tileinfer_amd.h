@@ -80,12 +80,17 @@ int ti_kv_append(const void* key, const void* value, int64_t key_row_stride,
  *   split_tokens > 0: fixed split-K -- one workgroup per (sequence, partition of split_tokens);
  *     outputs the split used, the maximum partitions per sequence, and the workspace (0 when every
  *     sequence fits one partition). The value must be a multiple of 32 and of page_size.
- *   split_tokens <= 0: balanced -- one round of workgroups (one KV-head wave per SIMD; whole
- *     further rounds when a run would exceed the block ids one workgroup stages) shares the
- *     batch's 16-token tiles evenly whatever the per-sequence lengths (sequences cut between
- *     workgroups are merged in a fixed order); outputs split_tokens_out = 0, max_splits_out = the
- *     number of runs per group of KV heads, and a workspace (the partials plus batch + 1 ints
- *     the merge reads) that also covers the scalar variant's own plan.
+ *   split_tokens <= 0: the MFMA variant's own choice.
+ *     - Short bounds (max_blocks_per_seq * page_size <= 1024 tokens) whose fixed partitions of
+ *       the smallest split (lcm(32, page_size) tokens) fit one round of workgroups (batch x
+ *       partitions x KV-head groups <= CUs): that fixed split, output as for split_tokens > 0.
+ *     - Otherwise balanced: one round of workgroups (one KV-head wave per SIMD; whole further
+ *       rounds when a run would exceed the block ids one workgroup stages) shares the batch's
+ *       16-token tiles evenly whatever the per-sequence lengths (sequences cut between
+ *       workgroups are merged in a fixed order); outputs split_tokens_out = 0, max_splits_out =
+ *       the number of runs per group of KV heads.
+ *     The workspace covers both plans and the scalar variant's own plan (the partials, plus
+ *     batch + 1 ints the balanced merge reads).
  * The plan depends only on host-known bounds, so it is valid for any seqlen values <=
  * max_blocks_per_seq * page_size and it is safe to compute once and reuse under graph capture.
  *

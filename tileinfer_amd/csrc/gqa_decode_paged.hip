@@ -959,13 +959,25 @@ int64_t lcm64(int64_t x, int64_t y) {
 // Launch plans of one decode call. `split`/`max_splits`/`ws_fixed`: one workgroup per
 // (sequence, partition of `split` tokens) -- the requested split, or the heuristic one for the
 // scalar variant. `balanced_wgs`/`ws_balanced`: the MFMA variant's balanced mode when no split was
-// requested (0 otherwise).
+// requested (0 otherwise). `short_split`/`short_splits`/`ws_short`: the MFMA variant's plan when no
+// split was requested and the context bound is short (0 otherwise; see plan()).
 struct Plan {
   int32_t split = 0, max_splits = 1, balanced_wgs = 0, chunk_min_tiles = 0;
-  int64_t ws_fixed = 0, ws_balanced = 0;
+  int32_t short_split = 0, short_splits = 0;
+  int64_t ws_fixed = 0, ws_balanced = 0, ws_short = 0;
 };
 
 constexpr int kMinChunkTiles = 4;  // 64 tokens: shorter runs are dominated by start-up
+// Short contexts: with a context bound of at most this many tokens, the MFMA variant's default is
+// fixed partitions of the smallest split (32 tokens at page size 16) whenever they fit one round
+// of workgroups. Each workgroup then knows its tokens from its grid position, so its block ids and
+// query are requested with its sequence length instead of after the balanced plan's scan, and the
+// merge needs no per-sequence first tile (graph time per call, same box, balanced -> fixed:
+// B = 1 x 512 12.7 -> 11.4 us, B = 16 x U[16, 512] 20.0 -> 14.8, B = 8 x 512 16.5 -> 13.3,
+// B = 64 x 128 19.9 -> 18.0, B = 8 x 1k 19.0 -> 18.3). At 2k-token bounds and above the balanced
+// plan is faster (B = 2 x 2k 18.5 against 18.8, B = 8 x 2k 24.1 against 33.9): each row is cut into
+// as many parts as the split allows and the merge reads them all.
+constexpr int64_t kShortBoundTokens = 1024;
 
 int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, int32_t max_blocks,
          int32_t split_req, Plan* out) {
@@ -1037,6 +1049,14 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
     out->chunk_min_tiles = int32_t(kMinChunkTiles < max_chunk ? kMinChunkTiles : max_chunk);
     // Partials, then the [batch + 1] first-tile entries (rounded to 256 bytes).
     out->ws_balanced = wgs * 2 * hq * (D + 2) * 4 + (int64_t(batch) * 4 + 4 + 255) / 256 * 256;
+    const int64_t wpb = (hkv % 4 == 0) ? 4 : (hkv % 2 == 0) ? 2 : 1;  // waves per workgroup
+    const int64_t short_splits = ceil_div(bound, unit);
+    if (bound > 0 && bound <= kShortBoundTokens &&
+        int64_t(batch) * short_splits * (hkv / wpb) <= cus) {
+      out->short_split = int32_t(unit);
+      out->short_splits = int32_t(short_splits);
+      out->ws_short = short_splits > 1 ? int64_t(batch) * hq * short_splits * (D + 2) * 4 : 0;
+    }
   }
   return TI_OK;
 }
@@ -1064,10 +1084,18 @@ extern "C" int ti_gqa_decode_plan(int32_t batch, int32_t num_q_heads, int32_t nu
     *max_splits_out = p.max_splits;
     *workspace_bytes_out = p.ws_fixed;
   } else {
-    // Balanced (MFMA) plan; the workspace also covers the scalar variant's fixed plan.
-    *split_tokens_out = 0;
-    *max_splits_out = p.balanced_wgs;
-    *workspace_bytes_out = p.ws_balanced > p.ws_fixed ? p.ws_balanced : p.ws_fixed;
+    // The MFMA variant's plan: fixed partitions for short bounds, else balanced. The workspace
+    // covers every plan of these bounds (the shared-prefix call's suffix decode is balanced, the
+    // scalar variant has its own split).
+    if (p.short_split > 0) {
+      *split_tokens_out = p.short_split;
+      *max_splits_out = p.short_splits;
+    } else {
+      *split_tokens_out = 0;
+      *max_splits_out = p.balanced_wgs;
+    }
+    const int64_t ws = p.ws_balanced > p.ws_fixed ? p.ws_balanced : p.ws_fixed;
+    *workspace_bytes_out = ws > p.ws_short ? ws : p.ws_short;
   }
   return TI_OK;
 }
@@ -1104,12 +1132,17 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
   int rc = plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq,
                 split_tokens, &pl);
   if (rc != TI_OK) return rc;
-  const bool balanced = kind != TI_DECODE_SCALAR && pl.balanced_wgs > 0;
-  const int32_t split = pl.split, max_splits = pl.max_splits;
+  // Short context bounds take fixed partitions by default (see plan()); not with prefix parts,
+  // whose balanced suffix decode leaves whole rows for the merge to fold them in parallel.
+  const bool short_fixed =
+      kind != TI_DECODE_SCALAR && split_tokens <= 0 && pl.short_split > 0 && pre_o == nullptr;
+  const bool balanced = kind != TI_DECODE_SCALAR && !short_fixed && pl.balanced_wgs > 0;
+  const int32_t split = short_fixed ? pl.short_split : pl.split;
+  const int32_t max_splits = short_fixed ? pl.short_splits : pl.max_splits;
   // Balanced calls with prefix parts keep one more part row per (sequence, q-head): whole
   // sequences leave their rows there for the merge.
   const bool whole_rows = balanced && pre_o != nullptr;
-  const int64_t ws_need = (balanced ? pl.ws_balanced : pl.ws_fixed) +
+  const int64_t ws_need = (balanced ? pl.ws_balanced : short_fixed ? pl.ws_short : pl.ws_fixed) +
                           (whole_rows ? prefixed_extra_bytes(batch, num_q_heads, head_dim) : 0);
   if (batch == 0) return TI_OK;
   if (!q || !k_cache || !v_cache || !block_table || !seqlen || !out) {
