@@ -775,9 +775,11 @@ def run_config(cfg: int, args, dev) -> dict:
         "metric": METRIC, "config": {"workload": f"config{cfg}", "batch": len(ctx),
                                      "ctx_min": min(ctx), "ctx_max": max(ctx), "ctx_sum": sum(ctx),
                                      "append_tokens": slots.numel(),
-                                     "partition": (f"balanced over {max_splits} workgroups"
-                                                   if split == 0 else
-                                                   f"fixed {split} tokens, up to {max_splits} per sequence"),
+                                     "partition": (f"fixed {split} tokens, up to {max_splits} per sequence"
+                                                   if split else
+                                                   f"balanced over {max_splits} workgroups"
+                                                   if max_splits else
+                                                   "one 4-wave workgroup per (KV head, sequence)"),
                                      "variant": args.variant},
         "decode_us": round(d_us, 2), "decode_GBps_algorithmic": round(d_bytes / (d_us * 1e-6) / 1e9, 1),
         "decode_pct_of_peak_hbm": round(100 * d_bytes / (d_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 2),

@@ -73,20 +73,30 @@ def test_balanced_plan_one_wave_per_simd_in_whole_rounds():
 def test_short_bounds_take_fixed_partitions():
     """With no split requested, context bounds of at most 1,024 tokens whose smallest fixed
     partitions fit one round of workgroups take that fixed split (lcm(32, page) tokens); longer
-    bounds, or batches whose partitions exceed one round, stay balanced. The workspace covers
-    every plan of the bounds (the balanced one is the largest here)."""
+    bounds, or batches whose partitions exceed one round, stay balanced. Bounds of at most 128
+    tokens whose (sequence, KV head) pairs fit one round take one workgroup per pair instead
+    (reported as split 0 over 0 runs). The workspace covers every plan of the bounds (the
+    balanced one is the largest here)."""
     ws_balanced = 256 * 2 * 24 * 258 * 4 + 256
     assert _plan(1, 24, 4, 256, 16, 32, 0) == (0, 32, 16, ws_balanced)      # config 1: 512 tokens
-    assert _plan(1, 24, 4, 256, 16, 64, 0)[:3] == (0, 32, 32)                # 1,024 tokens
-    assert _plan(1, 24, 4, 256, 16, 65, 0)[1] == 0                           # 1,040: balanced
+    assert _plan(1, 24, 4, 256, 16, 64, 0)[1:3] == (32, 32)                  # 1,024 tokens
+    assert _plan(1, 24, 4, 256, 16, 65, 0)[1:3] == (0, 256)                  # 1,040: balanced
     assert _plan(16, 24, 4, 256, 16, 32, 0)[1:3] == (32, 16)                 # 256 workgroups
-    assert _plan(17, 24, 4, 256, 16, 32, 0)[1] == 0                          # 272: balanced
-    assert _plan(1, 24, 4, 256, 8, 64, 0)[1:3] == (32, 16)                   # page 8, 512 tokens
-    assert _plan(2, 24, 4, 256, 64, 8, 0)[1:3] == (64, 8)                    # page 64: 64 tokens
-    assert _plan(32, 32, 8, 128, 16, 8, 0)[1:3] == (32, 4)                   # 2 KV-head groups
-    assert _plan(33, 32, 8, 128, 16, 8, 0)[1] == 0
+    assert _plan(17, 24, 4, 256, 16, 32, 0)[1:3] == (0, 256)                 # 272: balanced
+    assert _plan(5, 24, 4, 256, 8, 64, 0)[1:3] == (32, 16)                   # page 8, 512 tokens
+    assert _plan(5, 24, 4, 256, 64, 8, 0)[1:3] == (64, 8)                    # page 64: 512 tokens
+    assert _plan(16, 32, 8, 128, 16, 16, 0)[1:3] == (32, 8)                  # 2 KV-head groups
+    assert _plan(17, 32, 8, 128, 16, 16, 0)[1:3] == (0, 128)
+    # One workgroup per (sequence, KV head): up to 128 tokens, up to 256 pairs.
+    assert _plan(1, 24, 4, 256, 16, 8, 0)[1:3] == (0, 0)                     # 128 tokens
+    assert _plan(1, 24, 4, 256, 16, 9, 0)[1:3] == (32, 5)                    # 144: fixed
+    assert _plan(64, 24, 4, 256, 16, 8, 0)[1:3] == (0, 0)                    # 256 pairs
+    assert _plan(65, 24, 4, 256, 16, 8, 0)[1:3] == (0, 256)                  # 260 pairs: balanced
+    assert _plan(32, 32, 8, 128, 16, 4, 0)[1:3] == (0, 0)
+    assert _plan(1, 24, 4, 256, 8, 16, 0)[1:3] == (0, 0)                     # page 8, 128 tokens
     # A requested split is kept as it is.
     assert _plan(1, 24, 4, 256, 16, 32, 256)[1:3] == (256, 2)
+    assert _plan(1, 24, 4, 256, 16, 8, 32)[1:3] == (32, 4)
 
 
 @pytest.mark.parametrize("args,code", [

@@ -124,6 +124,9 @@ struct DecodeArgs {
   int32_t num_blocks32;  // block ids in [0, num_blocks32) are valid (int32 ids)
   int32_t hq, hkv, group, page_size, max_blocks, max_splits, split_tokens;
   int32_t page_log2;  // log2(page_size) when it is a power of two (the small-page path)
+  // 1: one workgroup per (KV head, sequence) whose waves split the sequence's tiles and combine
+  // their parts in LDS (no partials, no merge); 0 otherwise.
+  int32_t wave_split;
   float scale_log2;
   // Balanced mode (> 0): this many workgroups share the batch's 16-token tiles evenly (every
   // workgroup takes a contiguous run of the concatenated tiles of all sequences); partials are

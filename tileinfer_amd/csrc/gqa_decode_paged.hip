@@ -138,7 +138,10 @@ __device__ __forceinline__ int balanced_chunk(const DecodeArgs& a, int total_til
 // SMALL: pages of 1, 2, 4 or 8 tokens (a 16-token tile spans 16 / page_size pages, so each lane
 // addresses its own rows' pages with a 64-bit address); otherwise pages of a multiple of 16
 // tokens (a tile lies in one page: one buffer descriptor per tile).
-template <int D, typename Tag, int WPB, int POL, bool SMALL>
+// WS (wave split): one workgroup per (sequence, KV head) whose WPB waves take consecutive tile
+// ranges of the sequence and combine their parts through LDS (short contexts of small batches: no
+// merge launch). Otherwise each wave is one KV head of the workgroup's group.
+template <int D, typename Tag, int WPB, int POL, bool SMALL, bool WS = false>
 __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int batch) {
   constexpr int KK = D / 32;
   constexpr int NC = D / 128;
@@ -156,7 +159,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;  // MFMA row/col index: token row of K, head of S^T/O^T, d-col of V^T
   const int g = lane >> 4;  // MFMA k-group
-  const int kvh = blockIdx.x * WPB + wave;
+  const int kvh = WS ? int(blockIdx.x) : int(blockIdx.x) * WPB + wave;
   const int h = kvh * a.group + n;
   const bool head_ok = n < a.group;
 
@@ -337,17 +340,18 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     }
   };
 
-  // Attention of this wave's query group over tokens [t0, t1) of sequence b (16-aligned t0):
-  // leaves the unnormalised (o, m_run) and the head's denominator l_tot. Uniform over the
-  // workgroup (it stages the partition's block ids in LDS).
-  auto run_partition = [&](int b, int t0, int t1) {
+  // Attention of this wave's query group over tokens [w0, w1) of sequence b, inside the
+  // workgroup's partition [t0, t1) (16-aligned t0 and w0; w0 = t0, w1 = t1 unless WS): leaves the
+  // unnormalised (o, m_run) and the head's denominator l_tot. Uniform over the workgroup (it
+  // stages the partition's block ids in LDS). `ends` marks the wave whose tokens end the sequence.
+  auto run_partition = [&](int b, int t0, int t1, int w0, int w1, bool ends) {
     tok0 = t0;
-    tok1 = t1;
-    // Fused append: the partition that ends at the sequence's last token writes that token's K/V
-    // rows (this wave's KV head) before any of its tiles is loaded. Its own later loads of the
-    // row then see them (the stores are waited for below, before the first tile load); no other
-    // workgroup reads that row.
-    const bool appended = a.app_slot != nullptr && t1 == seq_len(a, b);
+    tok1 = w1;
+    // Fused append: the wave whose tokens end at the sequence's last token writes that token's
+    // K/V rows (its KV head) before any of its tiles is loaded. Its own later loads of the row
+    // then see them (the stores are waited for below, before the first tile load); no other wave
+    // or workgroup reads that row.
+    const bool appended = a.app_slot != nullptr && ends;
     if (appended) {
       const int slot = __builtin_amdgcn_readfirstlane(a.app_slot[b]);
       if (slot >= 0 && slot < a.app_num_slots && lane < D / 8) {  // uniform slot test
@@ -360,7 +364,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     }
     const int page0 = tok0 / a.page_size;
     // The plan keeps every partition within kBidSlots pages; the clamp only guards LDS.
-    const int npages = tok1 > tok0 ? min((tok1 - 1) / a.page_size - page0 + 1, kBidSlots) : 0;
+    const int npages = t1 > t0 ? min((t1 - 1) / a.page_size - page0 + 1, kBidSlots) : 0;
     // The sequence's first block id (cache policy), requested with the partition's block ids.
     const int first_id =
         (POL == kPolicyAuto && share_slots > 0 && npages > 0) ? a.block_table[b * a.bt_stride] : -1;
@@ -382,13 +386,13 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     l_run = 0.f;
     if (appended) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the appended rows are written
     // Two tiles in flight: the next tile's loads are issued before the current one is consumed.
-    const int ntiles = (tok1 - tok0 + 15) / 16;
+    const int ntiles = (w1 - w0 + 15) / 16;
     if (ntiles > 0) {
       Tile<D> ta, tb;
-      load_tile(ta, tok0);
+      load_tile(ta, w0);
       int it = 0;
       for (; it + 2 <= ntiles; it += 2) {
-        const int p0 = tok0 + 16 * it;
+        const int p0 = w0 + 16 * it;
         load_tile(tb, p0 + 16);
         compute_tile(ta);
         if (it + 2 < ntiles) load_tile(ta, p0 + 32);
@@ -490,6 +494,71 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     }
   };
 
+  if constexpr (WS) {
+    // One workgroup per (KV head, sequence b): wave w takes the tiles [w per, (w + 1) per) of the
+    // sequence; the parts are combined through LDS in wave order.
+    __shared__ float s_comb[WS ? WPB : 1][WS ? 4 * NT + 2 : 1][64];
+    const int b = blockIdx.z;
+    const int ctx = seq_len(a, b);
+    if constexpr (POL == kPolicyAuto) {
+      if (wave == 0) build_share_set();
+      __syncthreads();
+    }
+    const int ntiles = (ctx + 15) >> 4;
+    const int per = (ntiles + WPB - 1) / WPB;
+    const int w0 = min(wave * per * 16, ctx);
+    const int w1 = min((wave + 1) * per * 16, ctx);
+    const int owner = ntiles > 0 ? (ntiles - 1) / per : 0;  // the wave holding the last token
+    run_partition(b, 0, ctx, w0, w1, wave == owner);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_comb[wave][4 * t + r][lane] = o[t][r];
+    }
+    s_comb[wave][4 * NT][lane] = m_run;
+    s_comb[wave][4 * NT + 1][lane] = l_tot;
+    __syncthreads();
+    if (!head_ok) return;
+    // m = max m_s, w_s = 2^(m_s - m), out = sum_s w_s o_s / sum_s w_s l_s, in wave order.
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < WPB; ++w) mm = fmaxf(mm, s_comb[w][4 * NT][lane]);
+    float wt[WPB];
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < WPB; ++w) {
+      const float ms = s_comb[w][4 * NT][lane];
+      wt[w] = ms == -INFINITY ? 0.f : fast_exp2(ms - mm);
+      l += wt[w] * s_comb[w][4 * NT + 1][lane];
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t* orow = a.out + (int64_t(b) * a.hq + h) * D;
+    const uint16_t* grow = a.gate ? a.gate + b * a.gate_sb + int64_t(h) * a.gate_sh : nullptr;
+    // Output group (c, r): d = 128 c + 32 g + 8 r + e holds o[8 c + e][r]; groups dealt to waves.
+    for (int q = wave; q < 4 * NC; q += WPB) {
+      const int c = q >> 2, r = q & 3;
+      float acc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+      for (int w = 0; w < WPB; ++w) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += wt[w] * s_comb[w][4 * (8 * c + e) + r][lane];
+      }
+      u32x4 v;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = pack2(acc[2 * k] * inv, acc[2 * k + 1] * inv, Tag{});
+      const int d = 128 * c + 32 * g + 8 * r;
+      if (grow) {
+        const u32x4 gv = load16(grow + d);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = gate_mul2(v[k], gv[k], Tag{});
+      }
+      *reinterpret_cast<u32x4*>(orow + d) = v;
+    }
+    return;
+  }
+
   if (a.balanced_wgs == 0) {
     // One workgroup per (sequence, partition of split_tokens).
     const int split = blockIdx.y;
@@ -502,7 +571,8 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
       __syncthreads();
     }
     const int t0 = split * a.split_tokens;
-    run_partition(b, t0, min(t0 + a.split_tokens, ctx));
+    const int t1 = min(t0 + a.split_tokens, ctx);
+    run_partition(b, t0, t1, t0, t1, t1 == ctx);
     if (!head_ok) return;
     if (nsplit <= 1) store_out(b);
     else store_partial((int64_t(b) * a.hq + h) * a.max_splits + split);
@@ -594,7 +664,8 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
         a.seq_first_tile[b] = sb;
       }
       const int ctx = __builtin_amdgcn_readfirstlane(seq_len(a, b));
-      run_partition(b, 16 * t0, min(16 * t1, ctx));
+      const int p0 = 16 * t0, p1 = min(16 * t1, ctx);
+      run_partition(b, p0, p1, p0, p1, p1 == ctx);
       if (head_ok) {
         if (t0 == 0 && t1 == nb) {
           // With precomputed prefix parts a whole sequence's row goes to its own part slot and
@@ -910,6 +981,22 @@ void launch_mfma_pages(const DecodeArgs& a, int batch, int policy, hipStream_t s
   }
 }
 
+// Wave split: one 4-wave workgroup per (KV head, sequence), no merge.
+template <int D, typename Tag, bool SMALL>
+void launch_wave_split_pages(const DecodeArgs& a, int batch, int policy, hipStream_t stream) {
+  const dim3 grid(a.hkv, 1, batch);
+  if (policy == kPolicyKeep) {
+    hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, 4, kPolicyKeep, SMALL, true>), grid, dim3(256),
+                       0, stream, a, batch);
+  } else if (policy == kPolicyStream) {
+    hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, 4, kPolicyStream, SMALL, true>), grid,
+                       dim3(256), 0, stream, a, batch);
+  } else {
+    hipLaunchKernelGGL((decode_mfma_kernel<D, Tag, 4, kPolicyAuto, SMALL, true>), grid, dim3(256),
+                       0, stream, a, batch);
+  }
+}
+
 template <int D, typename Tag, int WPB>
 int launch_mfma(const DecodeArgs& a, int batch, int policy, hipStream_t stream) {
   if (a.page_size < 16) launch_mfma_pages<D, Tag, WPB, true>(a, batch, policy, stream);
@@ -925,6 +1012,11 @@ constexpr int kWideMergeBatch = 4;
 template <int D, typename Tag>
 int launch_decode(const DecodeArgs& a, int batch, int policy, hipStream_t stream) {
   int rc;
+  if (a.wave_split) {
+    if (a.page_size < 16) launch_wave_split_pages<D, Tag, true>(a, batch, policy, stream);
+    else launch_wave_split_pages<D, Tag, false>(a, batch, policy, stream);
+    return check_launch("ti_gqa_decode_paged (mfma, wave split)");
+  }
   if (a.hkv % 4 == 0) {
     rc = launch_mfma<D, Tag, 4>(a, batch, policy, stream);
   } else if (a.hkv % 2 == 0) {
@@ -964,6 +1056,7 @@ int64_t lcm64(int64_t x, int64_t y) {
 struct Plan {
   int32_t split = 0, max_splits = 1, balanced_wgs = 0, chunk_min_tiles = 0;
   int32_t short_split = 0, short_splits = 0;
+  bool wave_split = false;  // short bounds of small batches: one workgroup per (KV head, sequence)
   int64_t ws_fixed = 0, ws_balanced = 0, ws_short = 0;
 };
 
@@ -978,6 +1071,14 @@ constexpr int kMinChunkTiles = 4;  // 64 tokens: shorter runs are dominated by s
 // plan is faster (B = 2 x 2k 18.5 against 18.8, B = 8 x 2k 24.1 against 33.9): each row is cut into
 // as many parts as the split allows and the merge reads them all.
 constexpr int64_t kShortBoundTokens = 1024;
+// Bounds of at most this many tokens (2 tiles per wave) take one 4-wave workgroup per (KV head,
+// sequence) instead, when the pairs fit one round: the waves split the sequence's tiles and
+// combine their parts in LDS, so there is no partial to write and no merge launch (graph time per
+// call against the fixed split: B = 16 x 64 11.3 -> 6.8 us, B = 1 x 128 10.7 -> 7.8). With more
+// tiles per wave the split is slower: a wave keeps two tiles in flight, so its tiles are a chain
+// of memory latencies (B = 1 x 512 11.2 -> 14.4 us, B = 4 x 1k 14.6 -> 28.3; B = 16 x 256, 4 tiles
+// per wave, 13.6 -> 13.3).
+constexpr int64_t kWaveSplitBoundTokens = 128;
 
 int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, int32_t max_blocks,
          int32_t split_req, Plan* out) {
@@ -1056,6 +1157,7 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
       out->short_split = int32_t(unit);
       out->short_splits = int32_t(short_splits);
       out->ws_short = short_splits > 1 ? int64_t(batch) * hq * short_splits * (D + 2) * 4 : 0;
+      out->wave_split = bound <= kWaveSplitBoundTokens && int64_t(batch) * hkv <= cus;
     }
   }
   return TI_OK;
@@ -1087,7 +1189,10 @@ extern "C" int ti_gqa_decode_plan(int32_t batch, int32_t num_q_heads, int32_t nu
     // The MFMA variant's plan: fixed partitions for short bounds, else balanced. The workspace
     // covers every plan of these bounds (the shared-prefix call's suffix decode is balanced, the
     // scalar variant has its own split).
-    if (p.short_split > 0) {
+    if (p.wave_split) {
+      *split_tokens_out = 0;
+      *max_splits_out = 0;
+    } else if (p.short_split > 0) {
       *split_tokens_out = p.short_split;
       *max_splits_out = p.short_splits;
     } else {
@@ -1136,13 +1241,17 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
   // whose balanced suffix decode leaves whole rows for the merge to fold them in parallel.
   const bool short_fixed =
       kind != TI_DECODE_SCALAR && split_tokens <= 0 && pl.short_split > 0 && pre_o == nullptr;
+  const bool wave_split = short_fixed && pl.wave_split;
   const bool balanced = kind != TI_DECODE_SCALAR && !short_fixed && pl.balanced_wgs > 0;
   const int32_t split = short_fixed ? pl.short_split : pl.split;
   const int32_t max_splits = short_fixed ? pl.short_splits : pl.max_splits;
   // Balanced calls with prefix parts keep one more part row per (sequence, q-head): whole
   // sequences leave their rows there for the merge.
   const bool whole_rows = balanced && pre_o != nullptr;
-  const int64_t ws_need = (balanced ? pl.ws_balanced : short_fixed ? pl.ws_short : pl.ws_fixed) +
+  const int64_t ws_need = (balanced ? pl.ws_balanced
+                           : wave_split ? 0
+                           : short_fixed ? pl.ws_short
+                                         : pl.ws_fixed) +
                           (whole_rows ? prefixed_extra_bytes(batch, num_q_heads, head_dim) : 0);
   if (batch == 0) return TI_OK;
   if (!q || !k_cache || !v_cache || !block_table || !seqlen || !out) {
@@ -1184,6 +1293,7 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
   a.seq_first_tile =
       balanced && a.part_o ? reinterpret_cast<int32_t*>(a.part_ml + n_parts * 2) : nullptr;
   a.balanced_wgs = balanced ? pl.balanced_wgs : 0;
+  a.wave_split = wave_split ? 1 : 0;
   a.chunk_min_tiles = pl.chunk_min_tiles;
   a.num_blocks32 = int32_t(num_blocks < INT32_MAX ? num_blocks : INT32_MAX);
   a.hq = num_q_heads;
