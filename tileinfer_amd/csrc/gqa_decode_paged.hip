@@ -197,7 +197,27 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
   // its inserts without a barrier): the last wave, while wave 0 runs the balanced scan, so the
   // set costs no time on the start-up path; with one wave per workgroup, wave 0 after its scan.
   // The barrier at the end of the scan (or the one below, for fixed splits) publishes it.
-  auto build_share_set = [&]() {
+  // First block ids of sequences [j0, j0 + 512), one per lane and step (the loads issued
+  // together), and their inserts into the set.
+  auto share_load_chunk = [&](int j0, int (&ids)[8]) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + 64 * u + lane;
+      ids[u] = j < batch ? a.block_table[int64_t(j) * a.bt_stride] : -1;
+    }
+  };
+  auto share_insert_chunk = [&](const int (&ids)[8]) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (uint32_t(ids[u]) < uint32_t(a.num_blocks32)) {
+        share_insert(s_skey, s_scnt, share_slots, ids[u]);
+      }
+    }
+  };
+  // Clears the set and inserts every sequence's first block id; `first` holds the ids of the
+  // first 512 sequences when the caller has already requested them (one memory latency with its
+  // own loads), nullptr otherwise.
+  auto build_share_set = [&](const int (*first)[8] = nullptr) {
     if constexpr (POL == kPolicyAuto) {
       if (share_slots == 0) return;
       for (int e = lane; e < share_slots; e += 64) {
@@ -205,18 +225,13 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
         s_scnt[e] = 0;
       }
       for (int j0 = 0; j0 < batch; j0 += 8 * 64) {
+        if (j0 == 0 && first != nullptr) {
+          share_insert_chunk(*first);
+          continue;
+        }
         int ids[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {  // the chunk's loads issued together
-          const int j = j0 + 64 * u + lane;
-          ids[u] = j < batch ? a.block_table[int64_t(j) * a.bt_stride] : -1;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          if (uint32_t(ids[u]) < uint32_t(a.num_blocks32)) {
-            share_insert(s_skey, s_scnt, share_slots, ids[u]);
-          }
-        }
+        share_load_chunk(j0, ids);
+        share_insert_chunk(ids);
       }
     }
   };
@@ -340,46 +355,36 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     }
   };
 
-  // Attention of this wave's query group over tokens [w0, w1) of sequence b, inside the
-  // workgroup's partition [t0, t1) (16-aligned t0 and w0; w0 = t0, w1 = t1 unless WS): leaves the
-  // unnormalised (o, m_run) and the head's denominator l_tot. Uniform over the workgroup (it
-  // stages the partition's block ids in LDS). `ends` marks the wave whose tokens end the sequence.
-  auto run_partition = [&](int b, int t0, int t1, int w0, int w1, bool ends) {
-    tok0 = t0;
-    tok1 = w1;
-    // Fused append: the wave whose tokens end at the sequence's last token writes that token's
-    // K/V rows (its KV head) before any of its tiles is loaded. Its own later loads of the row
-    // then see them (the stores are waited for below, before the first tile load); no other wave
-    // or workgroup reads that row.
-    const bool appended = a.app_slot != nullptr && ends;
-    if (appended) {
-      const int slot = __builtin_amdgcn_readfirstlane(a.app_slot[b]);
-      if (slot >= 0 && slot < a.app_num_slots && lane < D / 8) {  // uniform slot test
-        const int64_t dst = int64_t(slot) * a.row_stride + kvh * D + 8 * lane;
-        const u32x4 kw = load16(a.app_k + b * a.app_k_sb + kvh * D + 8 * lane);
-        const u32x4 vw = load16(a.app_v + b * a.app_v_sb + kvh * D + 8 * lane);
-        *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.k_cache) + dst) = kw;
-        *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.v_cache) + dst) = vw;
-      }
+  // Fused append: the wave whose tokens end at the sequence's last token writes that token's K/V
+  // rows (its KV head) before any of its tiles is loaded. Its own later loads of the row then see
+  // them (`attend` waits for the stores before the first tile load); no other wave or workgroup
+  // reads that row.
+  auto append_row = [&](int b) {
+    const int slot = __builtin_amdgcn_readfirstlane(a.app_slot[b]);
+    if (slot >= 0 && slot < a.app_num_slots && lane < D / 8) {  // uniform slot test
+      const int64_t dst = int64_t(slot) * a.row_stride + kvh * D + 8 * lane;
+      const u32x4 kw = load16(a.app_k + b * a.app_k_sb + kvh * D + 8 * lane);
+      const u32x4 vw = load16(a.app_v + b * a.app_v_sb + kvh * D + 8 * lane);
+      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.k_cache) + dst) = kw;
+      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.v_cache) + dst) = vw;
     }
-    const int page0 = tok0 / a.page_size;
-    // The plan keeps every partition within kBidSlots pages; the clamp only guards LDS.
-    const int npages = t1 > t0 ? min((t1 - 1) / a.page_size - page0 + 1, kBidSlots) : 0;
-    // The sequence's first block id (cache policy), requested with the partition's block ids.
-    const int first_id =
-        (POL == kPolicyAuto && share_slots > 0 && npages > 0) ? a.block_table[b * a.bt_stride] : -1;
-    __syncthreads();  // the previous partition's tiles are done with s_bids
-    for (int i = threadIdx.x; i < npages; i += 64 * WPB) {
-      s_bids[i] = a.block_table[b * a.bt_stride + page0 + i];
-    }
-    __syncthreads();
-    choose_policy(first_id);
-    // Query group as the B operand of S^T = K . Q^T; rows beyond the group stay zero.
+  };
+
+  // Query group of sequence b as the B operand of S^T = K . Q^T; rows beyond the group stay zero.
+  auto load_q = [&](int b) {
     const uint16_t* qrow = a.q + b * a.q_sb + int64_t(h) * a.q_sh;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       qop[kk] = head_ok ? load16(qrow + 32 * kk + 8 * g) : u32x4{0u, 0u, 0u, 0u};
     }
+  };
+
+  // Attention of this wave's query group over tokens [w0, w1) (16-aligned w0), with the query
+  // loaded and the block ids of the workgroup's partition, from token t0 (16-aligned), staged in
+  // LDS: leaves the unnormalised (o, m_run) and the head's denominator l_tot.
+  auto attend = [&](int t0, int w0, int w1, bool appended) {
+    tok0 = t0;
+    tok1 = w1;
 #pragma unroll
     for (int t = 0; t < NT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     m_run = -INFINITY;
@@ -403,6 +408,60 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     // Sum the per-lane partial denominators of each head (lanes n, n+16, n+32, n+48).
     l_tot = l_run + __shfl_xor(l_run, 16, 64);
     l_tot += __shfl_xor(l_tot, 32, 64);
+  };
+
+  // Balanced runs: attention over tokens [t0, t1) of sequence b (16-aligned t0), staging the
+  // partition's block ids in LDS. Uniform over the workgroup. `ends`: t1 is the sequence's end.
+  auto run_partition = [&](int b, int t0, int t1, bool ends) {
+    const bool appended = a.app_slot != nullptr && ends;
+    if (appended) append_row(b);
+    const int page0 = t0 / a.page_size;
+    // The plan keeps every partition within kBidSlots pages; the clamp only guards LDS.
+    const int npages = t1 > t0 ? min((t1 - 1) / a.page_size - page0 + 1, kBidSlots) : 0;
+    // The sequence's first block id (cache policy), requested with the partition's block ids.
+    const int first_id =
+        (POL == kPolicyAuto && share_slots > 0 && npages > 0) ? a.block_table[b * a.bt_stride] : -1;
+    __syncthreads();  // the previous partition's tiles are done with s_bids
+    for (int i = threadIdx.x; i < npages; i += 64 * WPB) {
+      s_bids[i] = a.block_table[b * a.bt_stride + page0 + i];
+    }
+    __syncthreads();
+    choose_policy(first_id);
+    load_q(b);
+    attend(t0, t0, t1, appended);
+  };
+
+  // Fixed partitions and wave splits, whose tokens follow from the grid position: everything a
+  // workgroup needs before its first tile is requested together, before the sequence length is
+  // known (one memory latency instead of three): the query group, the block ids of `npages`
+  // pages from page0 (staged in LDS; the host bound, not the length), the sequence's first block
+  // id and, for the cache policy, the batch's (the share set, wave 0). Ends with a barrier;
+  // returns the sequence's first block id.
+  auto prologue = [&](int b, int page0, int npages) -> int {
+    load_q(b);
+    constexpr int kRegIds = 4;  // ids per thread held in registers; the rest after them
+    int ids_r[kRegIds];
+#pragma unroll
+    for (int k = 0; k < kRegIds; ++k) {
+      const int i = int(threadIdx.x) + k * 64 * WPB;
+      ids_r[k] = i < npages ? a.block_table[b * a.bt_stride + page0 + i] : -1;
+    }
+    const int first_id =
+        (POL == kPolicyAuto && share_slots > 0 && npages > 0) ? a.block_table[b * a.bt_stride] : -1;
+    int share_ids[8];
+    const bool share_wave = POL == kPolicyAuto && share_slots > 0 && wave == 0;
+    if (share_wave) share_load_chunk(0, share_ids);
+#pragma unroll
+    for (int k = 0; k < kRegIds; ++k) {
+      const int i = int(threadIdx.x) + k * 64 * WPB;
+      if (i < npages) s_bids[i] = ids_r[k];
+    }
+    for (int i = int(threadIdx.x) + kRegIds * 64 * WPB; i < npages; i += 64 * WPB) {
+      s_bids[i] = a.block_table[b * a.bt_stride + page0 + i];
+    }
+    if (share_wave) build_share_set(&share_ids);
+    __syncthreads();
+    return first_id;
   };
 
   auto store_out = [&](int b) {
@@ -500,16 +559,16 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     __shared__ float s_comb[WS ? WPB : 1][WS ? 4 * NT + 2 : 1][64];
     const int b = blockIdx.z;
     const int ctx = seq_len(a, b);
-    if constexpr (POL == kPolicyAuto) {
-      if (wave == 0) build_share_set();
-      __syncthreads();
-    }
+    const int first_id = prologue(b, 0, min(a.max_blocks, kBidSlots));
+    choose_policy(first_id);
     const int ntiles = (ctx + 15) >> 4;
     const int per = (ntiles + WPB - 1) / WPB;
     const int w0 = min(wave * per * 16, ctx);
     const int w1 = min((wave + 1) * per * 16, ctx);
     const int owner = ntiles > 0 ? (ntiles - 1) / per : 0;  // the wave holding the last token
-    run_partition(b, 0, ctx, w0, w1, wave == owner);
+    const bool appended = a.app_slot != nullptr && wave == owner;
+    if (appended) append_row(b);
+    attend(0, w0, w1, appended);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
 #pragma unroll
@@ -564,15 +623,19 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     const int split = blockIdx.y;
     const int b = blockIdx.z;
     const int ctx = seq_len(a, b);
+    const int t0 = split * a.split_tokens;
+    // The partition's pages up to the host bound (the length is not known yet).
+    const int t_end = min(t0 + a.split_tokens, a.max_blocks * a.page_size);
+    const int page0 = t0 / a.page_size;
+    const int first_id = prologue(
+        b, page0, t_end > t0 ? min((t_end - 1) / a.page_size - page0 + 1, kBidSlots) : 0);
     const int nsplit = (ctx + a.split_tokens - 1) / a.split_tokens;
     if (split >= (nsplit > 0 ? nsplit : 1)) return;  // uniform over the workgroup
-    if constexpr (POL == kPolicyAuto) {
-      if (wave == 0) build_share_set();
-      __syncthreads();
-    }
-    const int t0 = split * a.split_tokens;
+    choose_policy(first_id);
     const int t1 = min(t0 + a.split_tokens, ctx);
-    run_partition(b, t0, t1, t0, t1, t1 == ctx);
+    const bool appended = a.app_slot != nullptr && t1 == ctx;
+    if (appended) append_row(b);
+    attend(t0, t0, t1, appended);
     if (!head_ok) return;
     if (nsplit <= 1) store_out(b);
     else store_partial((int64_t(b) * a.hq + h) * a.max_splits + split);
@@ -664,8 +727,8 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
         a.seq_first_tile[b] = sb;
       }
       const int ctx = __builtin_amdgcn_readfirstlane(seq_len(a, b));
-      const int p0 = 16 * t0, p1 = min(16 * t1, ctx);
-      run_partition(b, p0, p1, p0, p1, p1 == ctx);
+      const int p1 = min(16 * t1, ctx);
+      run_partition(b, 16 * t0, p1, p1 == ctx);
       if (head_ok) {
         if (t0 == 0 && t1 == nb) {
           // With precomputed prefix parts a whole sequence's row goes to its own part slot and
@@ -757,10 +820,14 @@ __global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int 
   int nparts = 0;
   int first_part_slot1 = 0;  // balanced: the first part sits in slot 1 of its workgroup
   if (a.balanced_wgs == 0) {
-    const int ctx = seq_len(a, b);
-    nparts = (ctx + a.split_tokens - 1) / a.split_tokens;
-    if (nparts <= 1) return;
     slot0 = (int64_t(b) * a.hq + h) * a.max_splits;
+    if constexpr (W == 1) {
+      nparts = -1;  // the row's first parts are requested below, before its length is known
+    } else {
+      const int ctx = seq_len(a, b);
+      nparts = (ctx + a.split_tokens - 1) / a.split_tokens;
+      if (nparts <= 1) return;
+    }
   } else {
     const int nb = seq_tiles(a, b);
     if (nb == 0 && wave != 0) return;  // uniform: one wave writes what follows
@@ -885,12 +952,26 @@ __global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int 
   // depend on the weights, so one memory latency covers both. Past nparts the last part's row is
   // read again (a valid row) and left out of the sum. nburst is uniform; readfirstlane lets the
   // compiler see it, so these are plain vector loads.
+  // Fixed partitions (nparts < 0 here): the part slots follow from the host-known max_splits, so
+  // the first rows and (m, l) are requested with the row's length, one memory latency for all;
+  // slots past the row's parts hold no value of this call and are left out below.
+  const int spec = nparts < 0 ? a.max_splits : nparts;
   constexpr int kBurst = 16;
-  const int nburst = __builtin_amdgcn_readfirstlane(min(nparts, kBurst));
+  const int nburst = __builtin_amdgcn_readfirstlane(min(spec, kBurst));
   PartVec vb[kBurst];
 #pragma unroll
   for (int u = 0; u < kBurst; ++u) {
     vb[u] = *reinterpret_cast<const PartVec*>(a.part_o + part(min(u, nburst - 1)) * D + d0);
+  }
+  float ms_first = -INFINITY, ls_first = 0.f;  // (m, l) of part `lane`
+  if (lane < spec) {
+    ms_first = a.part_ml[2 * part(lane)];
+    ls_first = a.part_ml[2 * part(lane) + 1];
+  }
+  if (nparts < 0) {
+    const int ctx = seq_len(a, b);
+    nparts = (ctx + a.split_tokens - 1) / a.split_tokens;
+    if (nparts <= 1) return;
   }
   // Maximum over the parts' m (and the prefix parts'), lane-parallel; lane s keeps the (m, l) of
   // part s (parts 0-63) for the weights below.
@@ -900,8 +981,12 @@ __global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int 
     const int s = s0 + lane;
     float ms = -INFINITY;
     if (s < nparts) {
-      ms = a.part_ml[2 * part(s)];
-      if (s0 == 0) ls0 = a.part_ml[2 * part(s) + 1];
+      if (s0 == 0) {
+        ms = ms_first;
+        ls0 = ls_first;
+      } else {
+        ms = a.part_ml[2 * part(s)];
+      }
     }
     if (s0 == 0) ms0 = ms;
     m = fmaxf(m, ms);
