@@ -53,9 +53,9 @@ def test_wave_split_vs_oracle(ctx, dev):
             assert bool((out[b] == 0).all())
 
 
-def test_wave_split_head_dim_128_fp16_and_page_8(dev):
-    """8 KV heads at head_dim 128 (fp16), and pages of 8 tokens bitwise against page 16 on the
-    same memory (the waves split 16-token tiles whatever the page size)."""
+def test_wave_split_head_dim_128_fp16_and_small_pages(dev):
+    """8 KV heads at head_dim 128 (fp16), and pages of 8, 4, 2 and 1 tokens bitwise against
+    page 16 on the same memory (the waves split 16-token tiles whatever the page size)."""
     ctx = [120, 33]
     step = make_step(ctx, pool=_pool(ctx), seed=47, dtype=torch.float16, hq=32, hkv=8, d=128)
     say(f"decode wave split d128 fp16 ctx={ctx}")
@@ -64,16 +64,18 @@ def test_wave_split_head_dim_128_fp16_and_page_8(dev):
     assert_decode_close(out, _ref(step))
     ctx = [100, 60, 0, 77]
     step = make_step(ctx, pool=_pool(ctx), seed=48)
-    say(f"decode wave split page 8 ctx={ctx}")
     base = _call(step, dev)
     t = step.block_table
-    cols = torch.arange(t.shape[1] * 2)
-    t8 = torch.where(t[:, cols // 2] >= 0, t[:, cols // 2] * 2 + cols % 2, -1).to(torch.int32)
-    k8, v8 = step.k_cache.view(-1, 8, 4, 256), step.v_cache.view(-1, 8, 4, 256)
-    assert decode_plan(4, 24, 4, 256, 8, t8.shape[1])[:2] == (0, 0)
-    out8 = gqa_decode_paged_fn(step.q.to(dev), k8.to(dev), v8.to(dev), t8.to(dev),
-                               step.seqlen.to(dev), 8)
-    assert torch.equal(bits(base), bits(out8))
+    for page in (8, 4, 2, 1):
+        say(f"decode wave split page {page} ctx={ctx}")
+        r = 16 // page
+        cols = torch.arange(t.shape[1] * r)
+        tp = torch.where(t[:, cols // r] >= 0, t[:, cols // r] * r + cols % r, -1).to(torch.int32)
+        kp, vp = step.k_cache.view(-1, page, 4, 256), step.v_cache.view(-1, page, 4, 256)
+        assert decode_plan(4, 24, 4, 256, page, tp.shape[1])[:2] == (0, 0)
+        outp = gqa_decode_paged_fn(step.q.to(dev), kp.to(dev), vp.to(dev), tp.to(dev),
+                                   step.seqlen.to(dev), page)
+        assert torch.equal(bits(base), bits(outp)), page
 
 
 @pytest.mark.parametrize("ctx", [
