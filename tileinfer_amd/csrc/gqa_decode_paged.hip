@@ -556,7 +556,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
   if constexpr (WS) {
     // One workgroup per (KV head, sequence b): wave w takes the tiles [w per, (w + 1) per) of the
     // sequence; the parts are combined through LDS in wave order.
-    __shared__ float s_comb[WS ? WPB : 1][WS ? 4 * NT + 2 : 1][64];
+    __shared__ float s_comb[WPB][4 * NT + 2][64];  // each wave's o values, then m and l, per lane
     const int b = blockIdx.z;
     const int ctx = seq_len(a, b);
     const int first_id = prologue(b, 0, min(a.max_blocks, kBidSlots));
