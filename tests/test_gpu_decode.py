@@ -242,7 +242,7 @@ def test_long_context_32k(dev):
 
 def test_one_long_sequence_many_parts(dev):
     """One 100,003-token sequence: the balanced plan cuts it into one part per workgroup (far more
-    than 64), which the merge sums as four ordered quarters, the ragged tail tile included."""
+    than 64), which the merge sums as ordered ranges, one per wave, the ragged tail tile included."""
     say("decode 1 x 100003")
     step = make_step([100003], pool=6300, seed=1010)
     out, _, _ = gpu_step(step, dev)

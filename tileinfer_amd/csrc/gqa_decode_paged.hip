@@ -750,8 +750,8 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
 // out = sum w_s o_s / sum w_s l_s. In balanced mode it also writes the zero rows of empty
 // sequences (no workgroup covers them).
 // W > 1 (small balanced batches): W waves per row; a row cut into more than 64 parts has them
-// split into W contiguous quarters, each summed in order by one wave, the quarters then added in
-// wave order (deterministic; a row of 64 parts or fewer takes the one-wave path unchanged).
+// split into W contiguous ranges, each summed in order by one wave, the ranges then added in wave
+// order (deterministic; a row of 64 parts or fewer takes the one-wave path unchanged).
 template <int D, typename Tag, int W>
 __global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int batch) {
   constexpr int PER = D / 64;  // d-values per thread
@@ -883,6 +883,24 @@ __global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int 
       if (wave != 0) return;
     } else {
       __shared__ float s_red[W - 1][PER + 1][64];  // the other waves' sums (o, then l)
+      const int quarter = (nparts + W - 1) / W;
+      const int p0 = min(wave * quarter, nparts);
+      const int p1 = min(p0 + quarter, nparts);
+      // This wave's first 16 part rows and the (m, l) of its first 64 parts are requested with
+      // every part's maximum, so one memory latency covers all three.
+      const int cnt0 = __builtin_amdgcn_readfirstlane(min(64, p1 - p0));
+      PartVec v0[16];
+      float ms_own = -INFINITY, ls_own = 0.f;  // (m, l) of part p0 + lane
+      if (cnt0 > 0) {  // uniform
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          v0[u] = *reinterpret_cast<const PartVec*>(a.part_o + part(p0 + min(u, cnt0 - 1)) * D + d0);
+        }
+        if (lane < cnt0) {
+          ms_own = a.part_ml[2 * part(p0 + lane)];
+          ls_own = a.part_ml[2 * part(p0 + lane) + 1];
+        }
+      }
       float m = -INFINITY;
 #pragma unroll 4
       for (int s0 = 0; s0 < nparts; s0 += 64) {
@@ -898,19 +916,31 @@ __global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int 
       float l = 0.f;
       if (wave == 0 && me != -INFINITY) l = add_pre(m, acc);  // the prefix parts first
       if (m != -INFINITY) {
-        const int quarter = (nparts + W - 1) / W;
-        const int p0 = min(wave * quarter, nparts);
-        const int p1 = min(p0 + quarter, nparts);
         for (int s0 = p0; s0 < p1; s0 += 64) {
           const int s = s0 + lane;
           float w = 0.f, wl = 0.f;
           if (s < p1) {
-            const float ms = a.part_ml[2 * part(s)];
+            const float ms = s0 == p0 ? ms_own : a.part_ml[2 * part(s)];
             w = ms == -INFINITY ? 0.f : fast_exp2(ms - m);
-            wl = w * a.part_ml[2 * part(s) + 1];
+            wl = w * (s0 == p0 ? ls_own : a.part_ml[2 * part(s) + 1]);
           }
           const int cnt = __builtin_amdgcn_readfirstlane(min(64, p1 - s0));
-          for (int j0 = 0; j0 < cnt; j0 += 16) {
+          auto add_part = [&](int j, const PartVec& v) __attribute__((always_inline)) {
+            const float wj = __shfl(w, j, 64);
+            const float lj = __shfl(wl, j, 64);
+#pragma unroll
+            for (int q = 0; q < PER; ++q) acc[q] += wj * v[q];
+            l += lj;
+          };
+          int j0 = 0;
+          if (s0 == p0) {  // uniform: the first 16 rows, requested above
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+              if (u < cnt) add_part(u, v0[u]);  // uniform
+            }
+            j0 = 16;
+          }
+          for (; j0 < cnt; j0 += 16) {
             PartVec v[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
@@ -919,13 +949,7 @@ __global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int 
             }
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
-              if (j0 + u < cnt) {  // uniform
-                const float wj = __shfl(w, j0 + u, 64);
-                const float lj = __shfl(wl, j0 + u, 64);
-#pragma unroll
-                for (int q = 0; q < PER; ++q) acc[q] += wj * v[u][q];
-                l += lj;
-              }
+              if (j0 + u < cnt) add_part(j0 + u, v[u]);  // uniform
             }
           }
         }
@@ -1089,10 +1113,13 @@ int launch_mfma(const DecodeArgs& a, int batch, int policy, hipStream_t stream) 
   return check_launch("ti_gqa_decode_paged (mfma)");
 }
 
-// Balanced calls of at most this many sequences merge with 4 waves per row: only a few
-// sequences can each be cut into more than 64 parts, and the merge of such a row is a chain of
-// dependent loads that 4 waves shorten 4-fold (B = 1 at 128k: 256 parts per row).
+// Balanced calls of at most this many sequences merge with kWideMergeWaves waves per row: only a
+// few sequences can each be cut into more than 64 parts, and the merge of such a row is a chain
+// of dependent loads that the waves shorten (B = 1 at 128k: 256 parts per row). Graph time per
+// call against 4 waves: B = 1 x 32k 39.1 -> 37.1 us, B = 1 x 128k 95.9 -> 93.9, B = 2 x 64k
+// 92.0 -> 90.8; 16 waves (128 registers each) spill and are slower than 4.
 constexpr int kWideMergeBatch = 4;
+constexpr int kWideMergeWaves = 8;
 
 template <int D, typename Tag>
 int launch_decode(const DecodeArgs& a, int batch, int policy, hipStream_t stream) {
@@ -1111,8 +1138,8 @@ int launch_decode(const DecodeArgs& a, int batch, int policy, hipStream_t stream
   }
   if (rc != TI_OK) return rc;
   if (a.balanced_wgs > 0 && batch <= kWideMergeBatch) {
-    hipLaunchKernelGGL((decode_merge_kernel<D, Tag, 4>), dim3(a.hq, batch), dim3(256), 0, stream,
-                       a, batch);
+    hipLaunchKernelGGL((decode_merge_kernel<D, Tag, kWideMergeWaves>), dim3(a.hq, batch),
+                       dim3(64 * kWideMergeWaves), 0, stream, a, batch);
     return check_launch("ti_gqa_decode_paged (merge)");
   }
   if (a.balanced_wgs > 0 || a.max_splits > 1) {
