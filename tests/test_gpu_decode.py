@@ -396,6 +396,7 @@ def _shared_prefix_step(suffix, prefix, seed, hq=24, hkv=4, d=256, page=16):
     ([300, 300, 5], 512, 256),                   # a fixed split
     ([90] * 40, 4096, None),                     # many sequences, long prefix
     ([32] * 64, 1024, None),                     # every run covers two whole sequences
+    ([20000, 3], 1024, None),                    # B = 2: a row of ~250 parts, the 8-wave merge
 ])
 def test_shared_prefix_decode(suffix, prefix, split, dev):
     """shared_prefix_tokens: the prefix attended once for the batch and merged into each row —
