@@ -543,14 +543,35 @@ def _sdpa_flash_us(w, causal: bool, args) -> dict:
 
 
 def other_configs_decode(dev, args) -> dict:
-    """One decode launch of BASELINE configs 2, 4 and 5 at their stated sizes (their own seeded
-    caches, separate from the config-3 slab), timed with HIP events; config 2 is also checked
-    against the CPU oracle, config 5 is timed both plain (cache-keeping policy) and with
-    shared_prefix_tokens=8192."""
+    """One decode launch of BASELINE configs 1, 2, 4 and 5 at their stated sizes (their own seeded
+    caches, separate from the config-3 slab), timed with HIP events; config 1 (a few microseconds
+    of GPU work, below the wrapper's host time) also as GPU time per call in a captured graph;
+    configs 1 and 2 are also checked against the CPU oracle, config 5 is timed both plain
+    (cache-keeping policy) and with shared_prefix_tokens=8192."""
     from oracle.ref_torch import ref_gqa_decode_paged
     from tileinfer_amd import workloads as wl
 
     res = {}
+    st = wl.config1(device=dev)
+    ctx = st.seqlen.tolist()
+    call = functools.partial(gqa_decode_paged_fn, st.q, st.k_cache, st.v_cache, st.block_table,
+                             st.seqlen, BLOCK)
+    split, max_splits, _ = decode_plan(1, HQ, HKV, HEAD_DIM, BLOCK, st.block_table.shape[1])
+    g_us = _graph_us(call)
+    res["config1"] = {"batch": 1, "ctx_sum": sum(ctx), "decode_us": round(_time(call, args.steps,
+                                                                                 args.warmup), 2),
+                      "decode_us_graph": round(g_us, 2),
+                      "decode_GBps_algorithmic_graph": round(
+                          decode_bytes(ctx) / (g_us * 1e-6) / 1e9, 1),
+                      "partition": f"fixed {split} tokens, up to {max_splits} per sequence"
+                      if split else "balanced" if max_splits else "one workgroup per (KV head, "
+                      "sequence)"}
+    out = call()
+    ref = ref_gqa_decode_paged(st.q.cpu(), st.k_cache.cpu(), st.v_cache.cpu(),
+                               st.block_table.cpu(), st.seqlen.cpu(), BLOCK).float()
+    err = (out.float().cpu() - ref).abs()
+    res["config1"]["decode_within_tol"] = bool((err <= 2e-2 + 1e-2 * ref.abs()).all())
+    del st
     for cfg in (2, 4, 5):
         st = {2: wl.config2, 4: lambda device: wl.config4(device=device)[0],
               5: wl.config5}[cfg](device=dev)
