@@ -731,10 +731,13 @@ def run_config(cfg: int, args, dev) -> dict:
     ctx = st.seqlen.tolist()
     a_us = _time(lambda: store_kvcache(key, val, rows(kc), rows(vc), slots), args.steps, args.warmup)
     # No cache-policy hint, as the unchanged call site passes none: chosen on the device.
-    d_us = _time(lambda: gqa_decode_paged_fn(st.q, kc, vc, st.block_table, st.seqlen,
-                                             split_tokens=args.split_tokens,
-                                             variant=args.variant),
-                 args.steps, args.warmup)
+    decode = functools.partial(gqa_decode_paged_fn, st.q, kc, vc, st.block_table, st.seqlen,
+                               split_tokens=args.split_tokens, variant=args.variant)
+    d_us = _time(decode, args.steps, args.warmup)
+    # Back to back in a captured graph, as a serving loop replays its decode step: GPU time per
+    # call with no host time between calls (a launch after the GPU idled starts its XCDs up to
+    # ~4 us apart, which the event-timed figure of a small call includes).
+    g_us = _graph_us(decode)
     a_bytes = append_bytes(slots, HKV * HEAD_DIM)
     d_bytes = decode_bytes(ctx)
     # Parity and the CPU reference on this state (the timed append, then decode), before the
@@ -804,6 +807,8 @@ def run_config(cfg: int, args, dev) -> dict:
                                      "variant": args.variant},
         "decode_us": round(d_us, 2), "decode_GBps_algorithmic": round(d_bytes / (d_us * 1e-6) / 1e9, 1),
         "decode_pct_of_peak_hbm": round(100 * d_bytes / (d_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 2),
+        "decode_us_graph": round(g_us, 2),
+        "decode_pct_of_peak_hbm_graph": round(100 * d_bytes / (g_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 2),
         "append_us": round(a_us, 2), "append_GBps_algorithmic": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
         "us_per_layer_step": round(a_us + d_us, 2), **extra, **checks,
     }
