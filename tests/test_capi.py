@@ -299,6 +299,15 @@ def test_noalloc_decode_rejects_plans_beyond_its_scratch():
     # An empty batch that fits is a no-op.
     assert lib.ti_gqa_decode_paged_noalloc(None, 0, 0, None, None, None, 0, None, None, 0, 24,
                                            4, 256, 16, 0, 0, 0, 0, 0, None) == _lib.TI_OK
+    # The same heads with a 128-token bound (16 sequences, 8-page table) take one workgroup per
+    # (KV head, sequence) and no scratch, so the size check passes even though the balanced plan
+    # of this shape would not fit; the call then fails later for want of a device or pointers.
+    _lib.check(lib.ti_gqa_decode_plan(16, 128, 8, 256, 16, 8, 0, ctypes.byref(s),
+                                      ctypes.byref(m), ctypes.byref(w)))
+    assert (s.value, m.value) == (0, 0) and w.value > cap
+    rc = lib.ti_gqa_decode_paged_noalloc(None, 0, 0, None, None, None, 8, None, None, 16, 128,
+                                         8, 256, 16, 1024, 8, 0, 0, 0, None)
+    assert rc != _lib.TI_OK and b"scratch" not in lib.ti_last_error()
 
 
 def test_fused_append_decode_argument_errors_without_device():

@@ -1,6 +1,7 @@
 """ti_gqa_decode_paged_noalloc (the decode entry point that allocates nothing) through the C ABI,
 against ti_gqa_decode_paged with a caller workspace: bitwise equal on two calls in a row, the
-second with a smaller batch and shorter contexts, for the balanced plan and a fixed split."""
+second with a smaller batch and shorter contexts, for the balanced plan, a fixed split and the
+plans of short context bounds."""
 import pytest
 import torch
 
@@ -120,3 +121,40 @@ def test_noalloc_python_wrapper_refusals(dev):
     ref = gqa_decode_paged_fn(q, kc, vc, table, seqlen, 16)
     gqa_decode_paged_noalloc(q, kc, vc, table, seqlen, 16, out=out)
     assert torch.equal(bits(out), bits(ref))
+
+
+def _pool(ctx):
+    return sum((c + 15) // 16 for c in ctx) + 8
+
+
+def test_noalloc_short_bounds_two_calls(dev):
+    """Short context bounds take the same plans through the entry point that allocates nothing:
+    fixed 32-token partitions (split-K scratch), then one workgroup per (KV head, sequence) (no
+    scratch), bitwise equal to ti_gqa_decode_paged on two calls in a row, the second smaller. At
+    128 query heads over 8 KV heads the balanced plan of the same shape would need more than the
+    scratch; the short call is taken, not refused."""
+    lib = _lib.load()
+    scratch = lib.ti_gqa_decode_scratch_bytes()
+    cases = []
+    for name, ctx, seed, kw, split in (("short fixed (batch 6)", [512, 1, 0, 300, 999, 64], 46, {}, 32),
+                                       ("per pair (batch 3)", [100, 0, 127], 47, {}, 0),
+                                       ("per pair, 128/8 heads", [100, 60], 48,
+                                        {"hq": 128, "hkv": 8}, 0)):
+        cases.append((name, _on(make_step(ctx, pool=_pool(ctx), seed=seed, **kw), dev), split))
+    for name, step, split in cases:
+        b, hq = step.q.shape[:2]
+        hkv = step.k_cache.shape[2]
+        plan = decode_plan(b, hq, hkv, 256, 16, step.block_table.shape[1])
+        say(f"no-alloc decode short bound, {name}: plan {plan[:2]}")
+        assert plan[0] == split
+        if hq == 128:
+            assert plan[2] > scratch  # the plans' largest workspace: the balanced one
+        ref = gqa_decode_paged_fn(step.q, step.k_cache, step.v_cache, step.block_table,
+                                  step.seqlen, 16)
+        out = torch.full_like(step.q, float("nan"))
+        torch.cuda.synchronize()
+        before = torch.cuda.memory_allocated(dev)
+        _lib.check(_noalloc_abi(step, out, None, dev))
+        torch.cuda.synchronize()
+        assert torch.cuda.memory_allocated(dev) == before
+        assert torch.equal(bits(out), bits(ref)), name

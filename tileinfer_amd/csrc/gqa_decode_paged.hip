@@ -1279,6 +1279,31 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
 // row (o, then (m, l)) per (sequence, q-head) for the whole sequences.
 int64_t prefixed_extra_bytes(int64_t batch, int64_t hq, int64_t D) { return batch * hq * (D + 2) * 4; }
 
+// The launch shape a call takes from its plan, and the workspace that shape needs. Short context
+// bounds take fixed partitions by default (see plan()), up to kWaveSplitBoundTokens one workgroup
+// per (KV head, sequence) with no workspace; not with prefix parts, whose balanced suffix decode
+// leaves whole rows for the merge to fold them in parallel (one more part row per (sequence,
+// q-head)).
+struct EntryShape {
+  bool short_fixed, wave_split, balanced;
+  int64_t ws_need;
+};
+
+EntryShape entry_shape(const Plan& pl, int kind, int32_t split_tokens, bool prefixed,
+                       int32_t batch, int32_t num_q_heads, int32_t head_dim) {
+  EntryShape e;
+  e.short_fixed =
+      kind != TI_DECODE_SCALAR && split_tokens <= 0 && pl.short_split > 0 && !prefixed;
+  e.wave_split = e.short_fixed && pl.wave_split;
+  e.balanced = kind != TI_DECODE_SCALAR && !e.short_fixed && pl.balanced_wgs > 0;
+  e.ws_need = (e.balanced ? pl.ws_balanced
+               : e.wave_split ? 0
+               : e.short_fixed ? pl.ws_short
+                               : pl.ws_fixed) +
+              (e.balanced && prefixed ? prefixed_extra_bytes(batch, num_q_heads, head_dim) : 0);
+  return e;
+}
+
 }  // namespace
 }  // namespace ti
 
@@ -1349,22 +1374,16 @@ int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h, const vo
   int rc = plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq,
                 split_tokens, &pl);
   if (rc != TI_OK) return rc;
-  // Short context bounds take fixed partitions by default (see plan()); not with prefix parts,
-  // whose balanced suffix decode leaves whole rows for the merge to fold them in parallel.
-  const bool short_fixed =
-      kind != TI_DECODE_SCALAR && split_tokens <= 0 && pl.short_split > 0 && pre_o == nullptr;
-  const bool wave_split = short_fixed && pl.wave_split;
-  const bool balanced = kind != TI_DECODE_SCALAR && !short_fixed && pl.balanced_wgs > 0;
+  const EntryShape shape =
+      entry_shape(pl, kind, split_tokens, pre_o != nullptr, batch, num_q_heads, head_dim);
+  const bool short_fixed = shape.short_fixed;
+  const bool wave_split = shape.wave_split;
+  const bool balanced = shape.balanced;
   const int32_t split = short_fixed ? pl.short_split : pl.split;
   const int32_t max_splits = short_fixed ? pl.short_splits : pl.max_splits;
-  // Balanced calls with prefix parts keep one more part row per (sequence, q-head): whole
-  // sequences leave their rows there for the merge.
+  // Balanced calls with prefix parts: whole sequences leave their rows in the extra part rows.
   const bool whole_rows = balanced && pre_o != nullptr;
-  const int64_t ws_need = (balanced ? pl.ws_balanced
-                           : wave_split ? 0
-                           : short_fixed ? pl.ws_short
-                                         : pl.ws_fixed) +
-                          (whole_rows ? prefixed_extra_bytes(batch, num_q_heads, head_dim) : 0);
+  const int64_t ws_need = shape.ws_need;
   if (batch == 0) return TI_OK;
   if (!q || !k_cache || !v_cache || !block_table || !seqlen || !out) {
     return fail(TI_EINVAL, "ti_gqa_decode_paged: null pointer");
@@ -1595,8 +1614,9 @@ extern "C" int ti_gqa_decode_paged_noalloc(const void* q, int64_t q_stride_b, in
   int rc = plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq,
                 split_tokens, &pl);
   if (rc != TI_OK) return rc;
-  const bool balanced = (variant & 0xF) != TI_DECODE_SCALAR && pl.balanced_wgs > 0;
-  const int64_t need = balanced ? pl.ws_balanced : pl.ws_fixed;
+  // The shape ti_gqa_decode_paged would take, and so the scratch this call uses.
+  const int64_t need =
+      entry_shape(pl, variant & 0xF, split_tokens, false, batch, num_q_heads, head_dim).ws_need;
   if (need > kDecodeScratchBytes) {
     return fail(TI_EINVAL,
                 "ti_gqa_decode_paged_noalloc: this call needs %lld bytes of split-K scratch, the "
