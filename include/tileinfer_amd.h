@@ -409,8 +409,10 @@ int ti_gqa_decode_paged_prefixed(const void* q, int64_t q_stride_b, int64_t q_st
  * counterpart in the reference (its decode allocates its output and a padded block table on every
  * call, kernels/gqa_decode_paged.py:421-437). Same arguments and results as ti_gqa_decode_paged;
  * the split-K partials go to a static device array of ti_gqa_decode_scratch_bytes() bytes
- * (32 MiB) that each GPU the library runs on holds until the process ends. Calls whose plan needs
- * more (ti_gqa_decode_plan's workspace_bytes) return TI_EINVAL. Every call on one GPU shares that
+ * (32 MiB) that each GPU the library runs on holds until the process ends. Calls whose launch
+ * needs more (the workspace ti_gqa_decode_paged would use for the same call, of which
+ * ti_gqa_decode_plan's workspace_bytes, taken over every plan, is an upper bound) return
+ * TI_EINVAL. Every call on one GPU shares that
  * GPU's array: calls that overlap on one GPU (different streams, or host threads) race and must be
  * serialised by the caller. Allocates and frees nothing; the array's device address is looked up
  * once per device on the first call.
