@@ -77,12 +77,18 @@ __device__ __forceinline__ void issue_tile(Tile<D>& T, __amdgpu_buffer_rsrc_t rk
 
 // The batch's first-column block ids in an LDS hash set with a count per id, so that a sequence
 // can ask whether another sequence starts with the same block (kPolicyAuto). Open addressing with
-// linear probing over `slots` (a power of two, at least twice the ids inserted).
+// linear probing over `slots` (a power of two: four times the ids inserted, at most kShareSlots,
+// so at least twice).
 constexpr int kShareSlots = 4096;
 constexpr int kShareMaxBatch = kShareSlots / 2;
 
+// Multiplicative (Fibonacci) hashing: the top log2(slots) bits of id * 2^32 / phi, which depend on
+// every bit of the id. The product's low bits depend only on the id's low bits, and a free-list
+// allocator gives equal-length sequences first blocks k * L apart: with those, every id would
+// start its probe in one of a few slots (batch 256 at L = 512: probes of up to 256 slots, against
+// 1 here; simulated on the host).
 __device__ __forceinline__ uint32_t share_hash(int id, int slots) {
-  return (uint32_t(id) * 2654435761u) & uint32_t(slots - 1);
+  return (uint32_t(id) * 2654435761u) >> (32 - __builtin_ctz(uint32_t(slots)));
 }
 
 __device__ __forceinline__ void share_insert(int* keys, int* counts, int slots, int id) {
@@ -190,7 +196,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
     s_scnt = s_share_cnt;
     if (batch <= kShareMaxBatch && a.max_blocks > 0) {  // uniform
       share_slots = 64;
-      while (share_slots < 2 * batch) share_slots <<= 1;
+      while (share_slots < 4 * batch && share_slots < kShareSlots) share_slots <<= 1;
     }
   }
   // One wave fills the set (a wave's LDS operations take effect in order, so its clear precedes
