@@ -755,9 +755,10 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
 // workgroup, in workgroup order (deterministic): m = max m_s, w_s = 2^(m_s - m),
 // out = sum w_s o_s / sum w_s l_s. In balanced mode it also writes the zero rows of empty
 // sequences (no workgroup covers them).
-// W > 1 (small balanced batches): W waves per row; a row cut into more than 64 parts has them
-// split into W contiguous ranges, each summed in order by one wave, the ranges then added in wave
-// order (deterministic; a row of 64 parts or fewer takes the one-wave path unchanged).
+// W > 1 (balanced batches of at most kMidMergeBatch sequences): W waves per row; a row cut into
+// more than 64 parts has them split into W contiguous ranges, each summed in order by one wave,
+// the ranges then added in wave order (deterministic; a row of 64 parts or fewer takes the
+// one-wave path unchanged).
 template <int D, typename Tag, int W>
 __global__ __launch_bounds__(64 * W) void decode_merge_kernel(DecodeArgs a, int batch) {
   constexpr int PER = D / 64;  // d-values per thread
@@ -1119,13 +1120,23 @@ int launch_mfma(const DecodeArgs& a, int batch, int policy, hipStream_t stream) 
   return check_launch("ti_gqa_decode_paged (mfma)");
 }
 
-// Balanced calls of at most this many sequences merge with kWideMergeWaves waves per row: only a
-// few sequences can each be cut into more than 64 parts, and the merge of such a row is a chain
-// of dependent loads that the waves shorten (B = 1 at 128k: 256 parts per row). Graph time per
-// call against 4 waves: B = 1 x 32k 39.1 -> 37.1 us, B = 1 x 128k 95.9 -> 93.9, B = 2 x 64k
-// 92.0 -> 90.8; 16 waves (128 registers each) spill and are slower than 4.
+// Balanced calls of at most kWideMergeBatch sequences merge with kWideMergeWaves waves per row,
+// up to kMidMergeBatch with kMidMergeWaves. A sequence holding more than a quarter of the batch's
+// tiles is cut into more than 64 parts (up to 256), in any batch, and the merge of its rows is a
+// chain of dependent loads that the waves shorten; rows of 64 parts or fewer leave the extra waves
+// idle, and those occupy wave slots. Graph time per call, same box:
+// * 8 waves against 4 at one to four sequences: B = 1 x 32k 39.1 -> 37.1 us, B = 1 x 128k
+//   95.9 -> 93.9, B = 2 x 64k 92.0 -> 90.8 (16 waves, 128 registers each, spill and are slower).
+// * 4 waves against 1 above four: one 128k sequence and 4, 7 or 15 of 512 tokens 117.8 -> 97.8,
+//   118.4 -> 98.6, 120.9 -> 101.7 us; 64k + 15 x 1k 83.1 -> 68.0; 32k + 31 x 256 60.2 -> 45.2;
+//   uniform batches within 0.2 us (config 2, 16 x 8k, 32 x 2k). At 64 sequences 4 waves cost
+//   uniform batches more than they save (64 x 1k 51.6 -> 53.3; 32k + 63 x 512 64.0 -> 54.1): the
+//   1,536 rows' workgroups no longer fit one round of wave slots. 8 waves up to 32 sequences:
+//   +1.0-2.0 us on uniform batches.
 constexpr int kWideMergeBatch = 4;
 constexpr int kWideMergeWaves = 8;
+constexpr int kMidMergeBatch = 32;
+constexpr int kMidMergeWaves = 4;
 
 template <int D, typename Tag>
 int launch_decode(const DecodeArgs& a, int batch, int policy, hipStream_t stream) {
@@ -1146,6 +1157,11 @@ int launch_decode(const DecodeArgs& a, int batch, int policy, hipStream_t stream
   if (a.balanced_wgs > 0 && batch <= kWideMergeBatch) {
     hipLaunchKernelGGL((decode_merge_kernel<D, Tag, kWideMergeWaves>), dim3(a.hq, batch),
                        dim3(64 * kWideMergeWaves), 0, stream, a, batch);
+    return check_launch("ti_gqa_decode_paged (merge)");
+  }
+  if (a.balanced_wgs > 0 && batch <= kMidMergeBatch) {
+    hipLaunchKernelGGL((decode_merge_kernel<D, Tag, kMidMergeWaves>), dim3(a.hq, batch),
+                       dim3(64 * kMidMergeWaves), 0, stream, a, batch);
     return check_launch("ti_gqa_decode_paged (merge)");
   }
   if (a.balanced_wgs > 0 || a.max_splits > 1) {
