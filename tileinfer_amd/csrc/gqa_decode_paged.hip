@@ -82,8 +82,8 @@ __device__ __forceinline__ void issue_tile(Tile<D>& T, __amdgpu_buffer_rsrc_t rk
 constexpr int kShareSlots = 4096;
 constexpr int kShareMaxBatch = kShareSlots / 2;
 
-// Multiplicative (Fibonacci) hashing: the top log2(slots) bits of id * 2^32 / phi, which depend on
-// every bit of the id. The product's low bits depend only on the id's low bits, and a free-list
+// Multiplicative (Fibonacci) hashing: the top log2(slots) bits of id * 2654435761 (a prime near
+// 2^32 / phi) modulo 2^32, which depend on every bit of the id. The product's low bits depend only on the id's low bits, and a free-list
 // allocator gives equal-length sequences first blocks k * L apart: with those, every id would
 // start its probe in one of a few slots (batch 256 at L = 512: probes of up to 256 slots, against
 // 1 here; simulated on the host).
