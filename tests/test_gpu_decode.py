@@ -473,14 +473,15 @@ def test_shared_prefix_graph_capture_replay(dev):
 
 @pytest.mark.parametrize("ctx,waves", [
     ([40000] + [300] * 7, 4),       # B = 8: the long rows cut into ~230 parts, 4-wave merge
-    ([20000] + [200] * 31, 4),      # B = 32: the 4-wave merge's largest batch
-    ([24000] + [200] * 39, 1),      # B = 40: one wave per row, ~190 parts in bursts of 16
+    ([20000] + [200] * 31, 4),      # B = 32 (768 rows): the 4-wave merge's largest batch
+    ([24000] + [200] * 39, 2),      # B = 40: 2 waves per row, ~190 parts
+    ([24000] + [200] * 79, 1),      # B = 80 (1,920 rows): one wave, ~150 parts in bursts of 16
 ])
 def test_one_long_sequence_among_short_ones(ctx, waves, dev):
     """A batch whose first sequence holds most of the tiles: the balanced plan cuts its rows into
     more than 64 parts whatever the batch size, and the merge sums them with 4 waves per row up
-    to 32 sequences and with one above (8 up to 4 sequences, tested elsewhere). Against the
-    oracle; empty rows stay zero."""
+    to 768 rows (q-heads x sequences), 2 up to 1,536 and one above (8 up to 96 rows, tested
+    elsewhere). Against the oracle."""
     step = make_step(ctx, pool=sum((c + 15) // 16 for c in ctx) + 8, seed=73 + len(ctx))
     tiles = [(c + 15) // 16 for c in ctx]
     split, wgs, _ = decode_plan(len(ctx), 24, 4, 256, 16, step.block_table.shape[1])

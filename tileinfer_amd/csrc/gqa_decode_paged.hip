@@ -755,7 +755,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_mfma_kernel(DecodeArgs a, int
 // workgroup, in workgroup order (deterministic): m = max m_s, w_s = 2^(m_s - m),
 // out = sum w_s o_s / sum w_s l_s. In balanced mode it also writes the zero rows of empty
 // sequences (no workgroup covers them).
-// W > 1 (balanced batches of at most kMidMergeBatch sequences): W waves per row; a row cut into
+// W > 1 (balanced batches of at most kNarrowMergeRows rows): W waves per row; a row cut into
 // more than 64 parts has them split into W contiguous ranges, each summed in order by one wave,
 // the ranges then added in wave order (deterministic; a row of 64 parts or fewer takes the
 // one-wave path unchanged).
@@ -1120,11 +1120,13 @@ int launch_mfma(const DecodeArgs& a, int batch, int policy, hipStream_t stream) 
   return check_launch("ti_gqa_decode_paged (mfma)");
 }
 
-// Balanced calls of at most kWideMergeBatch sequences merge with kWideMergeWaves waves per row,
-// up to kMidMergeBatch with kMidMergeWaves. A sequence holding more than a quarter of the batch's
-// tiles is cut into more than 64 parts (up to 256), in any batch, and the merge of its rows is a
-// chain of dependent loads that the waves shorten; rows of 64 parts or fewer leave the extra waves
-// idle, and those occupy wave slots. Graph time per call, same box:
+// Balanced calls merge with 8 waves per row up to kWideMergeRows rows (q-heads x sequences), 4 up
+// to kMidMergeRows and 2 up to kNarrowMergeRows, one above. A sequence holding more than a quarter
+// of the batch's tiles is cut into more than 64 parts (up to 256), in any batch, and the merge of
+// its rows is a chain of dependent loads that the waves shorten; rows of 64 parts or fewer leave
+// the extra waves idle, and those occupy wave slots (the merge holds 160 VGPRs: 12 waves per CU,
+// 3,072 per round on 256 CUs, so rows x waves fit one round up to 1,536 rows at 2 waves and 768 at
+// 4). Graph time per call, same box (24 q-heads per sequence):
 // * 8 waves against 4 at one to four sequences: B = 1 x 32k 39.1 -> 37.1 us, B = 1 x 128k
 //   95.9 -> 93.9, B = 2 x 64k 92.0 -> 90.8 (16 waves, 128 registers each, spill and are slower).
 // * 4 waves against 1 above four: one 128k sequence and 4, 7 or 15 of 512 tokens 117.8 -> 97.8,
@@ -1133,10 +1135,11 @@ int launch_mfma(const DecodeArgs& a, int batch, int policy, hipStream_t stream) 
 //   uniform batches more than they save (64 x 1k 51.6 -> 53.3; 32k + 63 x 512 64.0 -> 54.1): the
 //   1,536 rows' workgroups no longer fit one round of wave slots. 8 waves up to 32 sequences:
 //   +1.0-2.0 us on uniform batches.
-constexpr int kWideMergeBatch = 4;
-constexpr int kWideMergeWaves = 8;
-constexpr int kMidMergeBatch = 32;
-constexpr int kMidMergeWaves = 4;
+// * 2 waves against 1 at 33 to 64 sequences: 32k + 63 x 512 66.0 -> 59.6 us, 32k + 47 x 512
+//   65.3 -> 57.6; uniform batches +0.1-0.25 us (64 x 1k 52.2 -> 52.4, 64 x 2k, 48 x 1k, 40 x 4k).
+constexpr int kWideMergeRows = 4 * 24;
+constexpr int kMidMergeRows = 32 * 24;
+constexpr int kNarrowMergeRows = 64 * 24;
 
 template <int D, typename Tag>
 int launch_decode(const DecodeArgs& a, int batch, int policy, hipStream_t stream) {
@@ -1154,14 +1157,16 @@ int launch_decode(const DecodeArgs& a, int batch, int policy, hipStream_t stream
     rc = launch_mfma<D, Tag, 1>(a, batch, policy, stream);
   }
   if (rc != TI_OK) return rc;
-  if (a.balanced_wgs > 0 && batch <= kWideMergeBatch) {
-    hipLaunchKernelGGL((decode_merge_kernel<D, Tag, kWideMergeWaves>), dim3(a.hq, batch),
-                       dim3(64 * kWideMergeWaves), 0, stream, a, batch);
-    return check_launch("ti_gqa_decode_paged (merge)");
-  }
-  if (a.balanced_wgs > 0 && batch <= kMidMergeBatch) {
-    hipLaunchKernelGGL((decode_merge_kernel<D, Tag, kMidMergeWaves>), dim3(a.hq, batch),
-                       dim3(64 * kMidMergeWaves), 0, stream, a, batch);
+  const int64_t rows = int64_t(a.hq) * batch;
+  if (a.balanced_wgs > 0 && rows <= kNarrowMergeRows) {
+    const dim3 grid(a.hq, batch);
+    if (rows <= kWideMergeRows) {
+      hipLaunchKernelGGL((decode_merge_kernel<D, Tag, 8>), grid, dim3(64 * 8), 0, stream, a, batch);
+    } else if (rows <= kMidMergeRows) {
+      hipLaunchKernelGGL((decode_merge_kernel<D, Tag, 4>), grid, dim3(64 * 4), 0, stream, a, batch);
+    } else {
+      hipLaunchKernelGGL((decode_merge_kernel<D, Tag, 2>), grid, dim3(64 * 2), 0, stream, a, batch);
+    }
     return check_launch("ti_gqa_decode_paged (merge)");
   }
   if (a.balanced_wgs > 0 || a.max_splits > 1) {
