@@ -1157,8 +1157,12 @@ int launch_decode(const DecodeArgs& a, int batch, int policy, hipStream_t stream
     rc = launch_mfma<D, Tag, 1>(a, batch, policy, stream);
   }
   if (rc != TI_OK) return rc;
+  // A row is cut into more than 64 parts only if its sequence spans more than 63 runs of the
+  // shortest chunk, which the table's bound tells; otherwise the extra waves would only idle.
   const int64_t rows = int64_t(a.hq) * batch;
-  if (a.balanced_wgs > 0 && rows <= kNarrowMergeRows) {
+  const int64_t bound_tiles = (int64_t(a.max_blocks) * a.page_size + 15) / 16;
+  if (a.balanced_wgs > 0 && rows <= kNarrowMergeRows &&
+      bound_tiles > int64_t(63) * a.chunk_min_tiles) {
     const dim3 grid(a.hq, batch);
     if (rows <= kWideMergeRows) {
       hipLaunchKernelGGL((decode_merge_kernel<D, Tag, 8>), grid, dim3(64 * 8), 0, stream, a, batch);
