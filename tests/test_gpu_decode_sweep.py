@@ -69,3 +69,28 @@ def test_decode_random_shape_vs_oracle(seed, dev):
         assert torch.equal(bits(fused), bits(out))
         assert torch.equal(bits(flat(kf)), bits(flat(kc))) and torch.equal(bits(flat(vf)),
                                                                            bits(flat(vc)))
+
+
+@pytest.mark.parametrize("batch", [3, 10, 40])
+@pytest.mark.parametrize("page", [8, 16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d", [128, 256])
+def test_long_row_merge_widths(d, dtype, page, batch, dev):
+    """One 6,000-token sequence among short ones: its rows are cut into ~94 parts, which the merge
+    sums with 8, 4 or 2 waves per row by the batch's row count (q-heads x sequences: 72-96, 240-
+    320, 960-1,280 here), for both head dims, both dtypes and pages of 8 and 16. The fused append
+    runs first. Against the oracle."""
+    hq, hkv = (24, 4) if d == 256 else (32, 8)
+    r = random.Random(batch * 1000 + page * 10 + d)
+    ctx = [6000] + [r.randint(0, 300) for _ in range(batch - 1)]
+    pool = sum(-(-c // page) for c in ctx) + 4
+    step = make_step(ctx, pool=pool, seed=batch + page + d, dtype=dtype, hq=hq, hkv=hkv, d=d,
+                     page=page)
+    plan = decode_plan(batch, hq, hkv, d, page, step.block_table.shape[1])
+    say(f"decode long-row merge: B={batch} hq={hq} d={d} page={page} {str(dtype)[6:]} "
+        f"plan={plan[:2]}")
+    assert plan[0] == 0 and plan[1] > 0  # balanced
+    out, kc, vc = gpu_step(step, dev)
+    ref, kr, vr = cpu_step(step)
+    assert torch.equal(bits(kc.cpu()), bits(kr))
+    assert_decode_close(out, ref)
