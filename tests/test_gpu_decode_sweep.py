@@ -4,7 +4,8 @@ itself, ragged) and the partition plan (the default for the shape, or an explici
 together, so that their combinations are checked and not only each one alone. Every case appends
 the step's token first (store_kvcache, then decode; the oracle does the same on CPU copies), and
 every other case also runs the decode with the append fused in (`append=`), which must give the
-same output and cache bit for bit."""
+same output and cache bit for bit. A second test runs one long sequence among short ones, whose
+rows the merge sums with 8, 4 or 2 waves, over head dims, dtypes and page sizes."""
 import random
 
 import pytest
