@@ -91,6 +91,11 @@ __device__ __forceinline__ void load_lds16(u32x4 rsrc, uint32_t voff, const uint
                : "memory");
 }
 
+// The cache row at byte offset `off` from `base`.
+__device__ __forceinline__ const uint16_t* at_bytes(const uint16_t* base, uint64_t off) {
+  return reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(base) + off);
+}
+
 // Buffer descriptor words of [base, base + bytes) (raw, no stride), uniform.
 __device__ __forceinline__ u32x4 rsrc_words(const uint16_t* base, uint32_t bytes) {
   const uint64_t addr = reinterpret_cast<uint64_t>(base);
@@ -378,6 +383,9 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     }
   }
   const uint32_t row_bytes = uint32_t(a.row_stride) * 2u;
+  // A page's bytes fit 32 bits (the host refuses larger pages), so a page's byte offset is one
+  // 32 x 32-bit product and the offsets inside a page are 32-bit.
+  const uint32_t page_bytes = uint32_t(a.page_stride) * 2u;
   // The sub-tile this wave loads (kKT / W rows per wave, inside one sub-tile).
   const int my_sub = (min(wave, LW - 1) * (kKT / LW)) / 16;
 
@@ -400,9 +408,10 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     else return key / a.page_size;
   };
   // Block ids of the next tile to load (uniform), fetched one tile ahead of their use; -1 for a
-  // sub-tile with nothing to load (past the context, or an absent page: masked, never loaded).
+  // sub-tile past the context. An id outside the cache is an absent page (masked, never loaded);
+  // the fetch that uses the id checks that, so nothing waits for the id's load before then.
   // The ids are read with scalar loads: a vector load would be counted with the K/V loads into
-  // LDS, and waiting for the ids (used right away) would then wait for the whole tile in flight.
+  // LDS, and waiting for the ids would then wait for the whole tile in flight.
   int nbid[NS];
   // SMALL: the next tile's present keys (bit 16 j + i: key i of sub-tile j is inside the context
   // and its page valid) and the block ids of the pages of this wave's sub-tile (-1: absent).
@@ -437,11 +446,15 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       nmask = live >= 64 ? mask : mask & ((uint64_t(1) << live) - 1);
       return;
     }
+    // Keys are non-negative, so the page's byte offset in the row is a 32-bit unsigned value
+    // (a scalar load with a register offset, no 64-bit address arithmetic).
+    typedef const __attribute__((address_space(4))) char* const_c_ptr;
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       const int key0 = k0 + 16 * j;
-      const int id = key0 < sx.kv_len ? row[page_of(key0)] : -1;
-      nbid[j] = uint32_t(id) < uint32_t(a.num_blocks32) ? id : -1;
+      const uint32_t pg = P2 ? uint32_t(key0) >> a.page_shift
+                             : uint32_t(key0) / uint32_t(a.page_size);
+      nbid[j] = key0 < sx.kv_len ? *(const_i32_ptr)((const_c_ptr)row + pg * 4u) : -1;
     }
   };
   // Keys of the sub-tile at key0 that exist (uniform).
@@ -479,40 +492,47 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
         const int id = pj == 0 ? nsid0 : pj == 1 ? nsid1 : pj == 2 ? nsid2 : nsid3;
         const int present = id < 0 ? 0 : min(max(sx.kv_len - (key_sub + pj * ps), 0), ps);
         const uint32_t nbytes = present > 0 ? uint32_t(present - 1) * row_bytes + D * 2 : 0u;
-        const int64_t base = int64_t(id < 0 ? 0 : id) * a.page_stride + int64_t(kvh) * D;
+        const uint64_t off = uint64_t(uint32_t(id < 0 ? 0 : id)) * page_bytes +
+                             uint32_t(kvh) * uint32_t(D * 2);
         // Offsets as the page-16 form computes them (relative to the sub-tile), moved to the
         // page's first row.
         const uint32_t ri = uint32_t(RPB * i) * row_bytes - uint32_t(pj * ps) * row_bytes;
         const uint32_t off_k = ((lane_k ^ uint32_t(16 * lds_swizzle(RPB * i))) + lane_hi) + ri;
         const uint32_t off_v = ((lane_v ^ uint32_t(16 * lds_swizzle_v(RPB * i))) + lane_hi) + ri;
         if constexpr (kAsmLoads) {
-          load_lds16(rsrc_words(a.k_cache + base, nbytes), off_k, sk + blk * 512);
-          load_lds16(rsrc_words(a.v_cache + base, nbytes), off_v, sv + blk * 512);
+          load_lds16(rsrc_words(at_bytes(a.k_cache, off), nbytes), off_k, sk + blk * 512);
+          load_lds16(rsrc_words(at_bytes(a.v_cache, off), nbytes), off_v, sv + blk * 512);
         } else {
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.k_cache + base, nbytes),
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(at_bytes(a.k_cache, off), nbytes),
                                                    (lds_ptr_t)(sk + blk * 512), 16, off_k, 0, 0, 0);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.v_cache + base, nbytes),
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(at_bytes(a.v_cache, off), nbytes),
                                                    (lds_ptr_t)(sv + blk * 512), 16, off_v, 0, 0, 0);
         }
       }
       return;
     }
+    // A sub-tile is empty past the context (id -1) or when its id is outside the cache.
+    auto absent = [&](int id) __attribute__((always_inline)) {
+      return uint32_t(id) >= uint32_t(a.num_blocks32);
+    };
     int bid = nbid[0];
-    uint32_t empty = nbid[0] < 0 ? 1u : 0u;
+    uint32_t empty = absent(nbid[0]) ? 1u : 0u;
 #pragma unroll
     for (int j = 1; j < NS; ++j) {
       if (my_sub == j) bid = nbid[j];
-      empty |= (nbid[j] < 0 ? 1u : 0u) << j;
+      empty |= (absent(nbid[j]) ? 1u : 0u) << j;
     }
     empty_out = empty;
     if (wave >= LW) return;  // uniform: the other waves only need the mask
     bid = __builtin_amdgcn_readfirstlane(bid);
     const int key0 = k0 + 16 * my_sub;
-    const int rows = __builtin_amdgcn_readfirstlane(bid < 0 ? 0 : sub_rows(key0));
-    bid = bid < 0 ? 0 : bid;
-    const int64_t base = int64_t(bid) * a.page_stride +
-                         int64_t(key0 - page_of(key0) * a.page_size) * a.row_stride +
-                         int64_t(kvh) * D;
+    const bool gone = absent(bid);
+    const int rows = __builtin_amdgcn_readfirstlane(gone ? 0 : sub_rows(key0));
+    bid = gone ? 0 : bid;
+    const uint32_t in_page = P2 ? uint32_t(key0) & uint32_t(a.page_size - 1)
+                                : uint32_t(key0 - page_of(key0) * a.page_size);
+    const uint64_t off = uint64_t(uint32_t(bid)) * page_bytes +
+                         (in_page * row_bytes + uint32_t(kvh) * uint32_t(D * 2));
     const uint32_t nbytes = rows > 0 ? uint32_t(rows - 1) * row_bytes + D * 2 : 0u;
     // Lean form: the per-lane offsets are recomputed at every fetch (an opaque copy of the lane
     // index keeps the compiler from hoisting 2 * LPW of them out of the loop, where they would
@@ -529,8 +549,8 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     // multiple of RPB LPW; q = ln / CPR; disjoint bit fields), and both swizzles are XOR-linear in
     // those bits, so each offset is a lane term, computed once per fetch, combined with a term of
     // i alone (an XOR-add and a scalar add per load, no 32-bit multiply).
-    const int q = ln / CPR;
-    const int slot = ln % CPR;
+    const int q = int(uint32_t(ln) / CPR);
+    const int slot = int(uint32_t(ln) % CPR);
     const int bw = (wblk * RPB) & 15;
     const uint32_t lane_hi = __umul24(uint32_t(bw | q), row_bytes);
     const uint32_t lane_k = uint32_t(slot ^ lds_swizzle(bw | q)) * 16u;
@@ -542,8 +562,8 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       off_v = ((lane_v ^ uint32_t(16 * lds_swizzle_v(RPB * i))) + lane_hi) + ri;
     };
     if constexpr (kAsmLoads) {
-      const u32x4 rk = rsrc_words(a.k_cache + base, nbytes);
-      const u32x4 rv = rsrc_words(a.v_cache + base, nbytes);
+      const u32x4 rk = rsrc_words(at_bytes(a.k_cache, off), nbytes);
+      const u32x4 rv = rsrc_words(at_bytes(a.v_cache, off), nbytes);
 #pragma unroll
       for (int i = 0; i < LPW; ++i) {
         const int blk = wblk + i;                  // 1 KiB block of the tile (uniform)
@@ -553,8 +573,8 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
         load_lds16(rv, off_v, sv + blk * 512);
       }
     } else {
-      const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k_cache + base, nbytes);
-      const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v_cache + base, nbytes);
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(at_bytes(a.k_cache, off), nbytes);
+      const __amdgpu_buffer_rsrc_t rv = make_rsrc(at_bytes(a.v_cache, off), nbytes);
 #pragma unroll
       for (int i = 0; i < LPW; ++i) {
         const int blk = wblk + i;
@@ -616,8 +636,14 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     }
     // A tile wholly below the wave's diagonal with every key present needs no mask (uniform).
     bool full = k0 + kKT - 1 <= wave_first_key;
+    if constexpr (SMALL) {
 #pragma unroll
-    for (int j = 0; j < NS; ++j) full = full && rows[j] == (SMALL ? 0xffff : 16);
+      for (int j = 0; j < NS; ++j) full = full && rows[j] == 0xffff;
+    } else {
+      // Every rows[j] == 16: the whole tile inside the context and no sub-tile empty (below the
+      // wave's first key every sub-tile is also at or below its last).
+      full = full && k0 + kKT <= sx.kv_len && empty == 0;
+    }
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       float v[4 * NS];
@@ -785,19 +811,17 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       const int k0 = (t0 + it) * kKT;
       // Stage 0 holds tile it; every wave is done with stage 1.
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (it + 1 < cnt) {
-        fetch(sk1, sv1, empty_st[1], k0 + kKT);
-        if (it + 2 < cnt) load_ids(k0 + 2 * kKT);
-      }
+      if (it + 1 < cnt) fetch(sk1, sv1, empty_st[1], k0 + kKT);
       if (k0 <= wave_last_key) compute(sk0, sv0, empty_st[0], k0);
+      // The ids of the tile after next, issued after this tile's LDS reads: the stage barrier's
+      // wait covers them, and the fetch after it is their first use.
+      if (it + 2 < cnt) load_ids(k0 + 2 * kKT);
       if (it + 1 >= cnt) break;
       // Stage 1 holds tile it + 1; every wave is done with stage 0.
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (it + 2 < cnt) {
-        fetch(sk0, sv0, empty_st[0], k0 + 2 * kKT);
-        if (it + 3 < cnt) load_ids(k0 + 3 * kKT);
-      }
+      if (it + 2 < cnt) fetch(sk0, sv0, empty_st[0], k0 + 2 * kKT);
       if (k0 + kKT <= wave_last_key) compute(sk1, sv1, empty_st[1], k0 + kKT);
+      if (it + 3 < cnt) load_ids(k0 + 3 * kKT);
     }
   };
 
@@ -1221,6 +1245,10 @@ int prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h, const v
     return fail(TI_EUNSUPPORTED,
                 "ti_gqa_prefill_paged: page_size %d is neither 4, 8 nor a multiple of 16",
                 page_size);
+  }
+  if (int64_t(num_kv_heads) * head_dim * page_size * 2 > int64_t(UINT32_MAX)) {
+    return fail(TI_EUNSUPPORTED, "ti_gqa_prefill_paged: a page of %d tokens x %d KV heads "
+                "exceeds 4 GiB", page_size, num_kv_heads);
   }
   if (key_splits < 1 || (key_splits > 1 && (workspace != nullptr || uo == nullptr)) ||
       int64_t(batch) * key_splits > 65535) {
