@@ -184,7 +184,8 @@ int ti_copy_blocks(const void* src, void* dst, const int64_t* block_pairs, int64
  *                gives every CU the same number of key tiles (units cut between workgroups are
  *                merged in a fixed order; deterministic, but not batch-invariant); three launches
  *                (schedule, attention, merge). The workspace is scratch of this call only.
- * Launches on `stream`. head_dim 128 or 256; page_size 4, 8 or a multiple of 16.
+ * Launches on `stream`. head_dim 128 or 256; page_size 4, 8 or a multiple of 16; a page of
+ * page_size x num_kv_heads x head_dim elements must fit 4 GiB (TI_EUNSUPPORTED otherwise).
  */
 int ti_gqa_prefill_paged(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                          const void* k_cache, const void* v_cache, const int32_t* block_table,

@@ -234,6 +234,11 @@ def test_prefill_argument_errors_without_device():
     for ps in (4, 8, 32):                           # accepted: fails later, on the null operands
         assert _prefill_abi(ps=ps) == _lib.TI_EINVAL, ps
     assert _prefill_abi(hq=25) == _lib.TI_EINVAL
+    # A page must fit 4 GiB (its byte offsets are 32-bit): 256 tokens x 32,768 KV heads x 256
+    # bf16 is exactly 4 GiB and refused; half the heads is accepted (then fails on null operands).
+    assert _prefill_abi(hq=32768, hkv=32768, ps=256) == _lib.TI_EUNSUPPORTED
+    assert b"4 GiB" in _lib.load().ti_last_error()
+    assert _prefill_abi(hq=16384, hkv=16384, ps=256) == _lib.TI_EINVAL
     rc = _prefill_abi()
     assert rc == _lib.TI_EINVAL and b"null" in _lib.load().ti_last_error()
 
