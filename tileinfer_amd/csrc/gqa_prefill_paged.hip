@@ -349,6 +349,10 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   __shared__ __align__(1024) uint16_t sv0[kKT * D];
   __shared__ __align__(1024) uint16_t sk1[kKT * D];
   __shared__ __align__(1024) uint16_t sv1[kKT * D];
+  // Pages of 16 tokens or more: each stage's empty sub-tiles (bit j), written by the loading
+  // wave 0 at the fetch and read by every wave after the next stage barrier, so that only the
+  // loading waves read the block ids.
+  __shared__ uint32_t s_empty[2];
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -446,6 +450,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       nmask = live >= 64 ? mask : mask & ((uint64_t(1) << live) - 1);
       return;
     }
+    if (wave >= LW) return;  // uniform: the other waves take the stage's mask from LDS
     // Keys are non-negative, so the page's byte offset in the row is a 32-bit unsigned value
     // (a scalar load with a register offset, no 64-bit address arithmetic).
     typedef const __attribute__((address_space(4))) char* const_c_ptr;
@@ -466,13 +471,18 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   // present keys instead (bit 16 j + i).
   typedef std::conditional_t<SMALL, uint64_t, uint32_t> StageMask;
   StageMask empty_st[2];
+  // The mask of stage st, valid after the stage barrier that follows its fetch.
+  auto stage_mask = [&](int st) __attribute__((always_inline)) -> StageMask {
+    if constexpr (SMALL) return empty_st[st];
+    else return StageMask(__builtin_amdgcn_readfirstlane(int(s_empty[st])));
+  };
   // Issue this wave's loads of the tile at key k0 into stage (sk, sv). A sub-tile lies in one
   // page; its loads use a buffer descriptor spanning only the rows that exist, so rows past the
   // context or in an absent page land in LDS as zero without a memory access.
-  auto fetch = [&](uint16_t* sk, uint16_t* sv, StageMask& empty_out, int k0)
+  auto fetch = [&](uint16_t* sk, uint16_t* sv, int st, int k0)
       __attribute__((always_inline)) {
     if constexpr (SMALL) {
-      empty_out = nmask;
+      empty_st[st] = nmask;
       if (wave >= LW) return;  // uniform: the other waves only need the mask
       const int ps = a.page_size;
       const int key_sub = k0 + 16 * my_sub;
@@ -511,6 +521,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       }
       return;
     }
+    if (wave >= LW) return;  // uniform: the other waves take the stage's mask from LDS
     // A sub-tile is empty past the context (id -1) or when its id is outside the cache.
     auto absent = [&](int id) __attribute__((always_inline)) {
       return uint32_t(id) >= uint32_t(a.num_blocks32);
@@ -522,8 +533,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       if (my_sub == j) bid = nbid[j];
       empty |= (absent(nbid[j]) ? 1u : 0u) << j;
     }
-    empty_out = empty;
-    if (wave >= LW) return;  // uniform: the other waves only need the mask
+    if (t == 0) s_empty[st] = empty;
     bid = __builtin_amdgcn_readfirstlane(bid);
     const int key0 = k0 + 16 * my_sub;
     const bool gone = absent(bid);
@@ -800,7 +810,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       }
     }
     if (cnt > 0) {
-      fetch(sk0, sv0, empty_st[0], t0 * kKT);
+      fetch(sk0, sv0, 0, t0 * kKT);
       if (cnt > 1) load_ids((t0 + 1) * kKT);
     }
     // Two tiles per trip so that each stage is a compile-time array. Each wave loads only part
@@ -811,16 +821,16 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       const int k0 = (t0 + it) * kKT;
       // Stage 0 holds tile it; every wave is done with stage 1.
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (it + 1 < cnt) fetch(sk1, sv1, empty_st[1], k0 + kKT);
-      if (k0 <= wave_last_key) compute(sk0, sv0, empty_st[0], k0);
+      if (it + 1 < cnt) fetch(sk1, sv1, 1, k0 + kKT);
+      if (k0 <= wave_last_key) compute(sk0, sv0, stage_mask(0), k0);
       // The ids of the tile after next, issued after this tile's LDS reads: the stage barrier's
       // wait covers them, and the fetch after it is their first use.
       if (it + 2 < cnt) load_ids(k0 + 2 * kKT);
       if (it + 1 >= cnt) break;
       // Stage 1 holds tile it + 1; every wave is done with stage 0.
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (it + 2 < cnt) fetch(sk0, sv0, empty_st[0], k0 + 2 * kKT);
-      if (k0 + kKT <= wave_last_key) compute(sk1, sv1, empty_st[1], k0 + kKT);
+      if (it + 2 < cnt) fetch(sk0, sv0, 0, k0 + 2 * kKT);
+      if (k0 + kKT <= wave_last_key) compute(sk1, sv1, stage_mask(1), k0 + kKT);
       if (it + 3 < cnt) load_ids(k0 + 3 * kKT);
     }
   };
