@@ -82,9 +82,10 @@ int ti_kv_append(const void* key, const void* value, int64_t key_row_stride,
  *     sequence fits one partition). The value must be a multiple of 32 and of page_size.
  *   split_tokens <= 0: the MFMA variant's own choice.
  *     - Bounds of at most 128 tokens whose (sequence, KV head) pairs fit one round (batch x
- *       num_kv_heads <= CUs): one 4-wave workgroup per pair, its waves splitting the sequence's
- *       tiles and combining their parts in LDS (no partials, no merge); outputs
- *       split_tokens_out = 0, max_splits_out = 0.
+ *       num_kv_heads <= CUs), and bounds of at most 512 tokens whose pairs fill three quarters
+ *       to all of one round (3/4 CUs <= batch x num_kv_heads <= CUs): one 4-wave workgroup per
+ *       pair, its waves splitting the sequence's tiles and combining their parts in LDS (no
+ *       partials, no merge); outputs split_tokens_out = 0, max_splits_out = 0.
  *     - Short bounds (max_blocks_per_seq * page_size <= 1024 tokens) whose fixed partitions of
  *       the smallest split (lcm(32, page_size) tokens) fit one round of workgroups (batch x
  *       partitions x KV-head groups <= CUs): that fixed split, output as for split_tokens > 0.

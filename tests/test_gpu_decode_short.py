@@ -1,8 +1,9 @@
-"""The decode plans for short context bounds: fixed 32-token partitions up to 1,024 tokens, and
-up to 128 tokens one 4-wave workgroup per (KV head, sequence) whose waves split the sequence's
-tiles and combine their parts in LDS. Both are checked against the CPU oracle and against explicit
-fixed partitions of the same data, with every wave count, empty sequences, head_dim 128, fp16,
-pages of 8 tokens, the gate epilogue, the fused append and graph replays."""
+"""The decode plans for short context bounds: fixed 32-token partitions up to 1,024 tokens, and one
+4-wave workgroup per (KV head, sequence) whose waves split the sequence's tiles and combine their
+parts in LDS, up to 128 tokens and, when the pairs fill three quarters to all of one round, up to
+512. Both are checked against the CPU oracle and against explicit fixed partitions of the same
+data, with every wave count, empty sequences, head_dim 128, fp16, pages of 8 tokens, the gate
+epilogue, the fused append and graph replays."""
 import pytest
 import torch
 
@@ -121,6 +122,59 @@ def test_wave_split_gate_and_fused_append(ctx, dev):
     ref_store_kvcache(step.k_new, step.v_new, flat(k_ref), flat(v_ref), step.slot_mapping)
     ref = ref_gqa_decode_paged(step.q, k_ref, v_ref, step.block_table, step.seqlen, 16)
     assert_decode_close(one, ref)
+
+
+def _ragged(b, lo, hi, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, hi + 1, (b,), generator=g).tolist()
+
+
+@pytest.mark.parametrize("ctx,hq,hkv,d,page,dtype", [
+    ([512] * 64, 24, 4, 256, 16, torch.bfloat16),             # 256 pairs: one full round
+    (_ragged(48, 0, 512, 61), 24, 4, 256, 16, torch.bfloat16),  # 192 pairs, ragged, empty rows
+    ([512] + [16] * 63, 24, 4, 256, 16, torch.bfloat16),       # one long sequence among short
+    (_ragged(32, 100, 400, 62), 32, 8, 128, 8, torch.float16),  # 256 pairs, head_dim 128, pages of 8
+])
+def test_pair_round_vs_oracle(ctx, hq, hkv, d, page, dtype, dev):
+    """Bounds of 129 to 512 tokens take one workgroup per (KV head, sequence) when those pairs
+    fill three quarters to all of one round: against the oracle and the explicit 32-token split."""
+    width = (max(ctx) + page - 1) // page
+    step = make_step(ctx, pool=_pool(ctx, page), seed=60 + len(ctx), width=width, hq=hq, hkv=hkv,
+                     d=d, dtype=dtype, page=page)
+    plan = decode_plan(len(ctx), hq, hkv, d, page, width)
+    say(f"decode pair round B={len(ctx)} hkv={hkv} d={d} page={page} bound={width * page} "
+        f"plan={plan[:2]}")
+    assert plan[:2] == (0, 0), "expected the one-workgroup-per-pair plan"
+    out = _call(step, dev)
+    assert_decode_close(out, _ref(step))
+    assert_decode_close(out, _call(step, dev, split_tokens=32))
+    for b, c in enumerate(ctx):
+        if c == 0:
+            assert bool((out[b] == 0).all())
+
+
+def test_pair_round_gate_and_fused_append(dev):
+    """At a 512-token bound with 256 pairs: the gate epilogue bitwise decode-then-gate, the fused
+    append bitwise store-then-decode."""
+    ctx = _ragged(64, 1, 512, 63)
+    step = make_step(ctx, pool=_pool(ctx), seed=64, width=32)
+    assert decode_plan(64, 24, 4, 256, 16, 32)[:2] == (0, 0)
+    say("decode pair round gate/append, B=64, bound 512")
+    g = torch.Generator().manual_seed(9)
+    gate = (3 * torch.randn(64, 1, 24 * 256, generator=g)).to(torch.bfloat16).to(dev)
+    plain = _call(step, dev)
+    gated = _call(step, dev, gate=gate)
+    assert torch.equal(bits(gated), bits(fused_sigmoid_mul(plain, gate.view(64, 24, 256))))
+    q, kn, vn = step.q.to(dev), step.k_new.to(dev), step.v_new.to(dev)
+    table, seqlen, slot = step.block_table.to(dev), step.seqlen.to(dev), step.slot_mapping.to(dev)
+    kc1, vc1 = step.k_cache.to(dev), step.v_cache.to(dev)
+    store_kvcache(kn, vn, flat(kc1), flat(vc1), slot)
+    two = gqa_decode_paged_fn(q, kc1, vc1, table, seqlen)
+    kc2, vc2 = step.k_cache.to(dev), step.v_cache.to(dev)
+    one = gqa_decode_paged_fn(q, kc2, vc2, table, seqlen, append=(kn, vn, slot))
+    torch.cuda.synchronize()
+    assert torch.equal(bits(one), bits(two))
+    assert torch.equal(bits(kc1), bits(kc2)) and torch.equal(bits(vc1), bits(vc2))
 
 
 def test_wave_split_graph_replays(dev):

@@ -129,14 +129,17 @@ def _pool(ctx):
 
 def test_noalloc_short_bounds_two_calls(dev):
     """Short context bounds take the same plans through the entry point that allocates nothing:
-    fixed 32-token partitions (split-K scratch), then one workgroup per (KV head, sequence) (no
-    scratch), bitwise equal to ti_gqa_decode_paged on two calls in a row, the second smaller. At
+    one workgroup per (KV head, sequence) for 64 sequences at a 512-token bound (no scratch), fixed
+    32-token partitions (split-K scratch), then per pair again at a 128-token bound, bitwise equal
+    to ti_gqa_decode_paged on calls in a row, each smaller than the one before. At
     128 query heads over 8 KV heads the balanced plan of the same shape would need more than the
     scratch; the short call is taken, not refused."""
     lib = _lib.load()
     scratch = lib.ti_gqa_decode_scratch_bytes()
     cases = []
-    for name, ctx, seed, kw, split in (("short fixed (batch 6)", [512, 1, 0, 300, 999, 64], 46, {}, 32),
+    for name, ctx, seed, kw, split in (("per pair, one round at a 512 bound (batch 64)",
+                                        [512] * 63 + [7], 49, {}, 0),
+                                       ("short fixed (batch 6)", [512, 1, 0, 300, 999, 64], 46, {}, 32),
                                        ("per pair (batch 3)", [100, 0, 127], 47, {}, 0),
                                        ("per pair, 128/8 heads", [100, 60], 48,
                                         {"hq": 128, "hkv": 8}, 0)):

@@ -1222,6 +1222,18 @@ constexpr int64_t kShortBoundTokens = 1024;
 // of memory latencies (B = 1 x 512 11.2 -> 14.4 us, B = 4 x 1k 14.6 -> 28.3; B = 16 x 256, 4 tiles
 // per wave, 13.6 -> 13.3).
 constexpr int64_t kWaveSplitBoundTokens = 128;
+// Bounds of at most this many tokens also take one workgroup per (KV head, sequence) when the
+// pairs fill three quarters to all of one round (192-256 on 256 CUs), whatever the fixed split
+// would need: every CU then streams one pair's pages, and neither partials nor a merge launch
+// are paid. Graph time per call, same box, against the plan these shapes took before (balanced):
+// B = 64 x 512 32.7 -> 25.0 us, 64 x U[16, 512] 28.1 -> 21.0, 64 x U[1, 512] 24.9 -> 20.8,
+// 48 x 512 30.1 -> 22.7, 56 x 384 26.4 -> 19.5, 64 x 256 23.0 -> 15.3, 64 x U[1, 256]
+// 24.4 -> 13.2. The cost is one long sequence among short ones, whose pair is a chain of up to 8
+// tiles per wave: 512 + 63 x 16 tokens 15.5 -> 19.0 us, 512 + 63 x 64 17.1 -> 19.4. Longer bounds
+// make that chain the whole call (2,048 + 63 x 64 tokens 19.3 -> 59.6 us; 64 x U[64, 2048]
+// 56.9 -> 67.1), so they keep the balanced plan, though uniform batches would gain (64 x 1k
+// 51.5 -> 46.5, 64 x 2k 90.0 -> 83.8).
+constexpr int64_t kPairRoundBoundTokens = 512;
 
 int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, int32_t max_blocks,
          int32_t split_req, Plan* out) {
@@ -1302,6 +1314,10 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
       out->ws_short = short_splits > 1 ? int64_t(batch) * hq * short_splits * (D + 2) * 4 : 0;
       out->wave_split = bound <= kWaveSplitBoundTokens && int64_t(batch) * hkv <= cus;
     }
+    if (bound > 0 && bound <= kPairRoundBoundTokens && int64_t(batch) * hkv * 4 >= cus * 3 &&
+        int64_t(batch) * hkv <= cus) {
+      out->wave_split = true;
+    }
   }
   return TI_OK;
 }
@@ -1311,10 +1327,10 @@ int plan(int32_t batch, int32_t hq, int32_t hkv, int32_t D, int32_t page_size, i
 int64_t prefixed_extra_bytes(int64_t batch, int64_t hq, int64_t D) { return batch * hq * (D + 2) * 4; }
 
 // The launch shape a call takes from its plan, and the workspace that shape needs. Short context
-// bounds take fixed partitions by default (see plan()), up to kWaveSplitBoundTokens one workgroup
-// per (KV head, sequence) with no workspace; not with prefix parts, whose balanced suffix decode
-// leaves whole rows for the merge to fold them in parallel (one more part row per (sequence,
-// q-head)).
+// bounds take fixed partitions by default (see plan()); one workgroup per (KV head, sequence), with
+// no workspace, up to kWaveSplitBoundTokens, and up to kPairRoundBoundTokens when the pairs fill
+// most of one round; not with prefix parts, whose balanced suffix decode leaves whole rows for
+// the merge to fold them in parallel (one more part row per (sequence, q-head)).
 struct EntryShape {
   bool short_fixed, wave_split, balanced;
   int64_t ws_need;
@@ -1325,8 +1341,8 @@ EntryShape entry_shape(const Plan& pl, int kind, int32_t split_tokens, bool pref
   EntryShape e;
   e.short_fixed =
       kind != TI_DECODE_SCALAR && split_tokens <= 0 && pl.short_split > 0 && !prefixed;
-  e.wave_split = e.short_fixed && pl.wave_split;
-  e.balanced = kind != TI_DECODE_SCALAR && !e.short_fixed && pl.balanced_wgs > 0;
+  e.wave_split = kind != TI_DECODE_SCALAR && split_tokens <= 0 && !prefixed && pl.wave_split;
+  e.balanced = kind != TI_DECODE_SCALAR && !e.short_fixed && !e.wave_split && pl.balanced_wgs > 0;
   e.ws_need = (e.balanced ? pl.ws_balanced
                : e.wave_split ? 0
                : e.short_fixed ? pl.ws_short

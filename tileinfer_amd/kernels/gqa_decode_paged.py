@@ -7,14 +7,15 @@ query token per sequence attends over ``seqlen_kv[b]`` cached tokens gathered th
 is a new ``[B, H_q, D]`` tensor in ``q``'s dtype.
 
 The work runs in libtileinfer_amd.so (``ti_gqa_decode_paged``): a split-K partial kernel on the
-gfx950 matrix cores plus a fixed-order merge, enqueued on the current stream. The plan follows
-from the table's width: balanced runs over the batch's tiles by default, fixed 32-token partitions
-for context bounds up to 1,024 tokens, and up to 128 tokens one workgroup per (KV head, sequence)
-whose waves combine their parts without a merge launch. The output and the split-K workspace come
-from torch's caching allocator, so the call is graph-capture safe. Unlike
-the reference wrapper it never pads the block table (kernels/gqa_decode_paged.py:421-430): any
-table width works, entries at or beyond ``ceil(seqlen/page_size)`` are never read, and block ids
-outside the cache at positions ``< seqlen`` are treated as absent instead of being read.
+gfx950 matrix cores plus a fixed-order merge, enqueued on the current stream. The plan follows from
+the table's width: balanced runs over the batch's tiles by default, fixed 32-token partitions for
+context bounds up to 1,024 tokens, and one workgroup per (KV head, sequence) whose waves combine
+their parts without a merge launch up to 128 tokens (up to 512 when those pairs fill three quarters
+to all of one round of workgroups). The output and the split-K workspace come from torch's caching
+allocator, so the call is graph-capture safe. Unlike the reference wrapper it never pads the block
+table (kernels/gqa_decode_paged.py:421-430): any table width works, entries at or beyond
+``ceil(seqlen/page_size)`` are never read, and block ids outside the cache at positions
+``< seqlen`` are treated as absent instead of being read.
 
 As in the reference, the caches are treated as flat ``[num_rows, H_kv, D]`` token rows grouped in
 pages of ``page_size`` rows (kernels/gqa_decode_paged.py:403-406), so ``page_size`` need not equal
