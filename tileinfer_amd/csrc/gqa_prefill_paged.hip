@@ -175,13 +175,17 @@ __device__ __forceinline__ int rows_key_end(const PrefillArgs& a, const SeqExten
 
 // Balanced schedule. A unit is (KV head, sequence, query block); its work is kUnitCost plus its key
 // tiles (the fixed part prices a unit's start-up and epilogue in tiles). Units are concatenated KV
-// head major, then by (sequence, query block) "pair", and workgroup i takes work [i * chunk,
-// (i + 1) * chunk) of the concatenation, so every workgroup gets the same work whatever the mix of
-// prompt and context lengths. A unit's key tiles sit at the end of its work; a unit cut between
+// head major, then by (sequence, query block) "pair", and run i of R takes work
+// [floor(i T / R), floor((i + 1) T / R)) of the concatenation's T, so every workgroup gets the same
+// work whatever the mix of prompt and context lengths (R: one per workgroup, fewer when a run
+// would be shorter than min_chunk tiles). A sequence's query blocks are listed shortest and
+// longest alternately (0, n - 1, 1, n - 2, ...): under a causal mask their works then sum in
+// pairs to about two runs, so run boundaries fall on every other unit's end and half as many
+// units are cut. A unit's key tiles sit at the end of its work; a unit cut between
 // workgroups is finished by each as an unnormalised partial (slot 0 when it is the workgroup's
 // first unit, 1 when its last) and merged afterwards in workgroup order. The tables, in the
 // workspace (int32):
-//   header   {pairs, work per KV head, chunk, total work}
+//   header   {pairs, work per KV head, runs, total work}
 //   per pair {sequence, query block, key tiles, exclusive prefix of work}   (max_pairs each)
 //   per workgroup {KV head, pair} of its first unit                        (balanced_wgs each)
 struct PlanView {
@@ -265,7 +269,9 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs 
         if (s_off[mid] <= p) lo = mid;
         else hi = mid;
       }
-      const int qb = p - s_off[lo];
+      const int k = p - s_off[lo];
+      const int nq = s_off[lo + 1] - s_off[lo];
+      const int qb = (k & 1) ? nq - 1 - (k >> 1) : (k >> 1);
       nt = (block_key_end(a, seq_extent(a, lo), qb * a.tq) + a.key_tile - 1) / a.key_tile;
       v.pair_b[p] = lo;
       v.pair_qb[p] = qb;
@@ -279,17 +285,17 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs 
   }
   const int64_t total = int64_t(a.hkv) * work;
   const int64_t wgs = a.balanced_wgs;
-  const int64_t chunk = max((total + wgs - 1) / wgs, int64_t(a.min_chunk));
+  const int64_t runs = max(int64_t(1), min(wgs, total / a.min_chunk));
   if (t == 0) {
     v.hdr[0] = n_pairs;
     v.hdr[1] = work;
-    v.hdr[2] = int32_t(chunk);
+    v.hdr[2] = int32_t(runs);
     v.hdr[3] = int32_t(total);
   }
   for (int i = t; i < wgs; i += kPlanThreads) v.wg_p[i] = -1;
   __syncthreads();  // the -1 defaults land before the starts below
-  // Workgroup i starts in the unit holding work position i * chunk (units without key tiles
-  // hold none; a position in a unit's fixed part starts that unit at its first key tile).
+  // Workgroup i starts in the unit holding work position floor(i * total / runs) (units without
+  // key tiles hold none; a position in a unit's fixed part starts that unit at its first key tile).
   const int units = a.hkv * n_pairs;
   for (int u = t; u < units; u += kPlanThreads) {
     const int kvh = u / n_pairs;
@@ -297,8 +303,8 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs 
     const int nt = v.pair_nt[p];
     if (nt == 0) continue;
     const int64_t pre = int64_t(kvh) * work + v.pair_pre[p];
-    for (int64_t i = (pre + chunk - 1) / chunk; i <= (pre + kUnitCost + nt - 1) / chunk && i < wgs;
-         ++i) {
+    const int64_t e = pre + kUnitCost + nt;  // the unit's work is [pre, e)
+    for (int64_t i = (pre * runs + total - 1) / total; i < runs && i * total / runs < e; ++i) {
       v.wg_kvh[i] = kvh;
       v.wg_p[i] = p;
     }
@@ -929,10 +935,10 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     kvh = __builtin_amdgcn_readfirstlane(v.wg_kvh[i]);
     n_pairs = __builtin_amdgcn_readfirstlane(v.hdr[0]);
     unit_work = __builtin_amdgcn_readfirstlane(v.hdr[1]);
-    const int64_t chunk = __builtin_amdgcn_readfirstlane(v.hdr[2]);
+    const int64_t runs = __builtin_amdgcn_readfirstlane(v.hdr[2]);
     const int64_t total = __builtin_amdgcn_readfirstlane(v.hdr[3]);
-    pos = int64_t(i) * chunk;
-    end = min(pos + chunk, total);
+    pos = int64_t(i) * total / runs;
+    end = int64_t(i + 1) * total / runs;
   }
   // A run that starts inside a unit defers that first piece (the unit's tail) to its end: every
   // run then starts at key 0 of a unit, and the deferred tail begins about where the run's last
@@ -1003,7 +1009,10 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
   const int n_pairs = v.hdr[0];
   if (p >= n_pairs) return;
   const int unit_work = v.hdr[1];
-  const int64_t chunk = v.hdr[2];
+  const int64_t runs = v.hdr[2];
+  const int64_t total = v.hdr[3];
+  // The run holding work position x: the last i with floor(i * total / runs) <= x.
+  auto run_of = [&](int64_t x) { return ((x + 1) * runs - 1) / total; };
   const int b = v.pair_b[p];
   const int qb0 = v.pair_qb[p] * a.tq;
   const int nt = v.pair_nt[p];
@@ -1012,12 +1021,12 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
   if (nt > 0) {
     const int64_t pre = int64_t(kvh) * unit_work + v.pair_pre[p];
     const int64_t k_pos = pre + kUnitCost;  // work position of the unit's first key tile
-    i0 = k_pos / chunk;
-    const int64_t i1 = (k_pos + nt - 1) / chunk;
+    i0 = run_of(k_pos);
+    const int64_t i1 = run_of(k_pos + nt - 1);
     if (i0 == i1) return;  // one workgroup finished the unit
     nparts = int(i1 - i0 + 1);
     // The first part is slot 1 of a workgroup that started in an earlier unit.
-    first_slot = i0 * chunk < pre ? 1 : 0;
+    first_slot = i0 * total / runs < pre ? 1 : 0;
   }
   const SeqExtent sx = seq_extent(a, b);
   const int rows = min(a.tq, sx.q_len - qb0) * a.group;
