@@ -424,9 +424,11 @@ def metric_extras(kv, tables, seqlen, q, dev, args) -> dict:
       store (kernels/kvcache_store.py:117-123); GPU time from a captured graph, since back-to-back
       eager calls of a few-µs kernel measure the Python wrapper;
     * the decode at the configured 2,048-token partitions (config 3) beside the balanced default;
-    * a batch-64 decode sweep over context 1k..32k (each sequence's first ctx/16 blocks of its
+    * a batch-64 decode sweep over context 256..32k (each sequence's first ctx/16 blocks of its
       permuted table), % of peak per point, as the reference's seqlen sweep
-      (kernels/gqa_decode_paged.py:614-656).
+      (kernels/gqa_decode_paged.py:614-656); up to 2k also the GPU time per call from a captured
+      graph, since an eager call of a few tens of µs partly measures the Python wrapper (at 256
+      and 512 tokens the 256 (sequence, KV head) pairs take one workgroup each).
     All timed with HIP events on the launch stream (mean over --steps calls after --warmup)."""
     k_rows, v_rows, k_paged, v_paged = layer_views(kv, 0)
     nb = k_paged.shape[0]
@@ -459,16 +461,21 @@ def metric_extras(kv, tables, seqlen, q, dev, args) -> dict:
         res[name] = {"ctx": full_ctx, "us": round(us, 2), "GBps_algorithmic": gbps(d_bytes, us),
                      "pct_of_peak_hbm": round(100 * d_bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 2)}
     sweep = []
-    ctx = 1024
+    ctx = 256
     while ctx <= full_ctx:
         tb = tables[0][:, :ctx // BLOCK]
         sl = torch.full((b,), ctx, dtype=torch.int32, device=dev)
-        us = _time(lambda: gqa_decode_paged_fn(q[0], k_paged, v_paged, tb, sl, BLOCK),
-                   args.steps, args.warmup)
+        fn = lambda: gqa_decode_paged_fn(q[0], k_paged, v_paged, tb, sl, BLOCK)  # noqa: E731
+        us = _time(fn, args.steps, args.warmup)
         nbytes = decode_bytes([ctx] * b)
-        sweep.append({"ctx": ctx, "us": round(us, 2), "GBps_algorithmic": gbps(nbytes, us),
-                      "pct_of_peak_hbm": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
-                                               2)})
+        point = {"ctx": ctx, "us": round(us, 2), "GBps_algorithmic": gbps(nbytes, us),
+                 "pct_of_peak_hbm": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 2)}
+        if ctx <= 2048:
+            ug = _graph_us(fn)
+            point["us_graph"] = round(ug, 2)
+            point["pct_of_peak_hbm_graph"] = round(
+                100 * nbytes / (ug * 1e-6) / 1e9 / PEAK_HBM_GBPS, 2)
+        sweep.append(point)
         ctx *= 2
     res["decode_ctx_sweep_batch64"] = sweep
     res["other_configs"] = other_configs_decode(dev, args)
