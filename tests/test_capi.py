@@ -319,19 +319,12 @@ def test_decode_plan_per_pair_round_rule_without_device():
     """Bounds of at most 512 tokens take one workgroup per (KV head, sequence) when those pairs
     fill three quarters to all of one round (no device here: the library assumes 256 CUs), and
     the balanced plan just outside either edge."""
-    lib = _lib.load()
-
-    def plan(batch, hq, hkv, d, page, width):
-        s, m, w = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
-        _lib.check(lib.ti_gqa_decode_plan(batch, hq, hkv, d, page, width, 0, ctypes.byref(s),
-                                          ctypes.byref(m), ctypes.byref(w)))
-        return s.value, m.value
-    assert plan(64, 24, 4, 256, 16, 32) == (0, 0)     # 256 pairs at a 512-token bound
-    assert plan(48, 24, 4, 256, 16, 32) == (0, 0)     # 192 pairs: three quarters
-    assert plan(32, 32, 8, 128, 8, 50) == (0, 0)      # 256 pairs, pages of 8, a 400-token bound
-    assert plan(47, 24, 4, 256, 16, 32) == (0, 256)   # 188 pairs: balanced
-    assert plan(65, 24, 4, 256, 16, 32) == (0, 256)   # 260 pairs: more than one round
-    assert plan(64, 24, 4, 256, 16, 33) == (0, 256)   # a 528-token bound
+    assert _plan(64, 24, 4, 256, 16, 32, 0)[:3] == (0, 0, 0)     # 256 pairs, a 512-token bound
+    assert _plan(48, 24, 4, 256, 16, 32, 0)[:3] == (0, 0, 0)     # 192 pairs: three quarters
+    assert _plan(32, 32, 8, 128, 8, 50, 0)[:3] == (0, 0, 0)      # pages of 8, a 400-token bound
+    assert _plan(47, 24, 4, 256, 16, 32, 0)[:3] == (0, 0, 256)   # 188 pairs: balanced
+    assert _plan(65, 24, 4, 256, 16, 32, 0)[:3] == (0, 0, 256)   # 260 pairs: over one round
+    assert _plan(64, 24, 4, 256, 16, 33, 0)[:3] == (0, 0, 256)   # a 528-token bound
 
 
 def test_fused_append_decode_argument_errors_without_device():
