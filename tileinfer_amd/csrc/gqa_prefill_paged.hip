@@ -407,6 +407,9 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   SeqExtent sx;
   const int32_t* bt_row = a.block_table;
   int wave_last_key = 0, wave_first_key = 0;
+  // Pages of 16 tokens or more: the last tile start whose tile needs no mask for the wave (every
+  // key inside the context and at or below every row's diagonal), one value per unit.
+  int full_k0 = 0;
   bool row_ok[C];
   int q_pos[C];
   u32x4 qop[C][KK];
@@ -651,14 +654,15 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
       }
     }
     // A tile wholly below the wave's diagonal with every key present needs no mask (uniform).
-    bool full = k0 + kKT - 1 <= wave_first_key;
+    bool full;
     if constexpr (SMALL) {
+      full = k0 + kKT - 1 <= wave_first_key;
 #pragma unroll
       for (int j = 0; j < NS; ++j) full = full && rows[j] == 0xffff;
     } else {
       // Every rows[j] == 16: the whole tile inside the context and no sub-tile empty (below the
       // wave's first key every sub-tile is also at or below its last).
-      full = full && k0 + kKT <= sx.kv_len && empty == 0;
+      full = k0 <= full_k0 && empty == 0;
     }
 #pragma unroll
     for (int c = 0; c < C; ++c) {
@@ -799,6 +803,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
     const int wave_row = min(ur - 1, (wave + 1) * 16 * C - 1);
     wave_last_key = a.causal ? sx.offset + (qr0 + wave_row) / G : INT32_MAX;
     wave_first_key = a.causal ? sx.offset + (qr0 + wave * 16 * C) / G : INT32_MAX;
+    full_k0 = min(wave_first_key - (kKT - 1), sx.kv_len - kKT);
     bt_row = a.block_table + int64_t(b) * a.bt_stride;
     const int cnt = t1 - t0;
     if (cnt > 0) load_ids(t0 * kKT);
