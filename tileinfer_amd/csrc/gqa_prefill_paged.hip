@@ -912,7 +912,7 @@ __global__ __launch_bounds__(64 * W) void prefill_mfma_kernel(PrefillArgs a) {
   const bool balanced = a.balanced_wgs > 0;
   // Balanced runs are dealt to the XCDs in contiguous blocks: workgroup ids go round-robin over
   // the 8 XCDs, so run i = (id % 8) * (G / 8) + id / 8 keeps consecutive runs (one KV head,
-  // neighbouring query blocks, the same K/V pages) in one XCD's L2.
+  // query blocks of one sequence, the same K/V pages) in one XCD's L2.
   const int nwg = a.balanced_wgs;
   const int i = (nwg % kXcds == 0) ? int(blockIdx.x % kXcds) * (nwg / kXcds) + int(blockIdx.x / kXcds)
                                    : int(blockIdx.x);
